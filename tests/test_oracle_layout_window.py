@@ -1,0 +1,138 @@
+"""Pin the oracle's packing layout, window rules and writer semantics (CPU only)."""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import codec, layout, window
+from mla_kv_quant_amd import synth
+
+
+@pytest.mark.parametrize("width", [128, 256, 512])
+def test_pack_roundtrip_and_independent_packer(width):
+    rng = np.random.default_rng(width)
+    codes = rng.integers(0, 4, size=(37, width), dtype=np.uint8)
+    packed = layout.pack_codes(codes)
+    assert packed.shape == (37, width // 4)
+    assert np.array_equal(layout.unpack_codes(packed, width), codes)
+    assert np.array_equal(packed, layout.pack_codes_bitwise(codes))
+
+
+def test_pack_hand_vectors():
+    # D = 128 (one group): the layout is the natural LSB-first packing
+    c = np.zeros((1, 128), np.uint8)
+    c[0, 0], c[0, 5], c[0, 127] = 1, 3, 2
+    p = layout.pack_codes(c)[0]
+    assert p[0] == 0b01 and p[1] == 0b11 << 2 and p[31] == 0b10 << 6
+    # D = 512: element 128 + 16*2 + 5 is group 1, word 2, code 5 -> word 4*2+1 = 9
+    c = np.zeros((1, 512), np.uint8)
+    c[0, 128 + 32 + 5] = 3
+    p = layout.pack_codes(c)[0]
+    assert np.flatnonzero(p).tolist() == [37] and p[37] == 3 << 2
+    # the 16 bytes 16s .. 16s+15 hold word s of every group
+    c = np.zeros((1, 512), np.uint8)
+    for g in range(4):
+        c[0, 128 * g + 16 * 3: 128 * g + 16 * 4] = g
+    p = layout.pack_codes(c)[0]
+    assert np.flatnonzero(p).min() >= 48 and np.flatnonzero(p).max() < 64
+    with pytest.raises(ValueError):
+        layout.pack_codes(np.full((1, 128), 4, np.uint8))
+
+
+def test_ring_row_and_keep_closed_form():
+    P, W, max_reqs = 4, 16, 8
+    for req in (0, 3, 7):
+        for pos in range(0, 80):
+            r = int(window.ring_row(req, pos, P, W))
+            base = 1 + req * (P + W)
+            assert base <= r < base + P + W
+            if pos < P:
+                assert r == base + pos
+            else:
+                assert r == base + P + (pos - P) % W
+    # slot 0 (graph padding) never claims a ring row; invalid requests neither
+    k = window.keep_mask([0, 0, 0, 5], [1, 1, 1, 100], [0, -1, 8, 0], [0, 3, 3, 3], P, W, max_reqs)
+    assert k.tolist() == [False, False, False, False]
+    seq = np.arange(1, 60)
+    k = window.keep_mask(seq - 1, seq, np.zeros_like(seq), np.ones_like(seq), P, W, max_reqs)
+    assert k.all()  # a decode write is always in the recent window
+
+
+def test_target_window_state_brute_force():
+    rng = np.random.default_rng(1)
+    for _ in range(50):
+        B, L = 3, int(rng.integers(1, 40))
+        P, W = int(rng.integers(0, 6)), int(rng.integers(0, 20))
+        valid = rng.random((B, L)) < 0.8
+        state = window.target_window_state(torch.from_numpy(valid), P, W).numpy()
+        for b in range(B):
+            idx = np.flatnonzero(valid[b])
+            for j in range(L):
+                if not valid[b, j]:
+                    exp = 0
+                else:
+                    rank = int(np.searchsorted(idx, j))
+                    exp = 1 if rank < P or rank >= len(idx) - W else 2
+                assert state[b, j] == exp
+        # unpadded rows follow the positional read rule
+        s = window.target_window_state(torch.ones(1, L, dtype=torch.bool), P, W).numpy()[0]
+        assert np.array_equal(s == 1, window.positional_bf16(np.arange(L), L, P, W))
+
+
+def test_window_transitions_match_reference_golden(golden_dir):
+    g = np.load(golden_dir / "window_golden.npz")
+    P, W, prompt = int(g["P"]), int(g["W"]), int(g["prompt"])
+    keys = torch.from_numpy(g["keys"]).view(torch.bfloat16)  # [B, 1, T, D]
+    pad = torch.from_numpy(g["pad"])
+    B, _, T, D = keys.shape
+    step = 0
+    while f"state{step}" in g:
+        hi = prompt + step
+        state = window.target_window_state(pad[:, :hi], P, W)
+        ref_state = torch.from_numpy(g[f"state{step}"])
+        assert torch.equal(state, ref_state)
+        # cache contents: state 2 rows are the bf16 QDQ of the original row
+        k_ref = torch.from_numpy(g[f"k{step}"]).view(torch.bfloat16)[:, 0]
+        orig = keys[:, 0, :hi]
+        _, _, _, qdq = codec.lloyd_codec(orig.float().reshape(-1, D))
+        qdq = qdq.reshape(B, hi, D).to(torch.bfloat16)
+        expect = torch.where((state == 2)[..., None], qdq, orig)
+        assert torch.equal(expect.view(torch.int16), k_ref.view(torch.int16))
+        step += 1
+    assert step >= 2
+
+
+def test_writer_oracle_semantics():
+    D, R, P, W, max_reqs = 512, 64, 4, 16, 4
+    pool = window.new_pool(300, D, R, max_reqs, P, W)
+    rot = synth.make_rotation(D, 1)
+    # prefill 40 tokens of request 2 into slots 101..140 (positions 0..39)
+    n = 40
+    x = synth.make_latent(n, D, 5, seed=2)
+    pe = synth.make_normal((n, R), 3)
+    loc = np.arange(101, 101 + n)
+    c = window.write_rows(pool, x, pe, loc, np.full(n, n), np.full(n, 2), rot, 0.98, 1.16,
+                          P, W, max_reqs, positions=np.arange(n))
+    codes, scale, zero, _ = codec.lloyd_codec(c, 128, 0.98, 1.16)
+    assert np.array_equal(layout.unpack_codes(pool["codes"][loc], D), codes.numpy())
+    assert np.array_equal(pool["params"][loc, :, 0], scale.numpy())
+    kept = [p for p in range(n) if p < P or p >= n - W]
+    for p in range(n):
+        row = pool["row_of_slot"][loc[p]]
+        if p in kept:
+            assert row == window.ring_row(2, p, P, W)
+            assert pool["owner_of_row"][row] == loc[p]
+        else:
+            assert row == -1
+    # decode step: position 40 evicts position 24's ring row (same (pos - P) % W)
+    x1 = synth.make_latent(1, D, 5, seed=4)
+    window.write_rows(pool, x1, synth.make_normal((1, R), 5), [141], [41], [2], rot, 0.98, 1.16,
+                      P, W, max_reqs)
+    r40 = window.ring_row(2, 40, P, W)
+    assert r40 == window.ring_row(2, 24, P, W)
+    assert pool["owner_of_row"][r40] == 141
+    # slot 0 writes codes but no rope / ownership
+    before = pool["owner_of_row"].copy()
+    window.write_rows(pool, x1, synth.make_normal((1, R), 6), [0], [42], [2], rot, 0.98, 1.16,
+                      P, W, max_reqs)
+    assert np.array_equal(before, pool["owner_of_row"]) and pool["row_of_slot"][0] == -1
