@@ -1,0 +1,126 @@
+/*
+ * rolaq_mla.h -- C ABI of the MI355X (gfx950) packed-INT2 RoLaQ MLA cache path.
+ *
+ * Every entry point takes raw device pointers, sizes and a HIP stream
+ * (hipStream_t passed as void*; NULL = the null stream). The caller owns all
+ * memory; nothing here allocates device memory, synchronises the stream or
+ * branches on device data on the host, so every launch is graph-capturable.
+ * Return value: ROLAQ_OK, or an error code with a message from
+ * rolaq_last_error() (thread-local). Invalid arguments are rejected before any
+ * launch and leave every buffer untouched.
+ *
+ * bf16 tensors are passed as void* holding IEEE bfloat16 bit patterns.
+ * Strides are in elements. Index tensors use the dtypes SGLang hands over.
+ *
+ * Cache layout per layer (num_slots token slots, D = kv_lora_rank, R = rope
+ * dim, NG = D / 128 quantization groups, P sink + W recent BF16 rows):
+ *   codes        uint8  [num_slots, D / 4]  2-bit codes; group g owns the
+ *                32-bit words NG*s + g (s = 0..7), element 16s+p of the group
+ *                at bits 2p of its word.
+ *   params       fp32   [num_slots, NG, 2]  (scale, zero) per group
+ *   rope_buf     bf16   [num_slots, R]
+ *   hp_c         bf16   [1 + max_reqs * (P + W), D]  rotated latent of the
+ *                sink/recent rows; ring row of (req, pos) is
+ *                1 + req*(P+W) + (pos < P ? pos : P + (pos - P) % W)
+ *   row_of_slot  int32  [num_slots]  ring row or -1 (shared by all layers)
+ *   owner_of_row int32  [1 + max_reqs * (P + W)]  slot owning a ring row
+ */
+#ifndef ROLAQ_MLA_H
+#define ROLAQ_MLA_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define ROLAQ_OK 0
+#define ROLAQ_ERR_INVALID 1 /* argument rejected; nothing launched */
+#define ROLAQ_ERR_HIP 2     /* a HIP launch failed */
+
+/* Message of the last error on the calling thread ("" if none). */
+const char* rolaq_last_error(void);
+
+/* ABI version of this library (bumped on any signature change). */
+int rolaq_abi_version(void);
+
+/*
+ * Quantize FP32 rows that are already in the rotated frame into the packed
+ * cache: Lloyd INT2 codes (thresholds -t, 0, +t on the group-normalised value),
+ * FP32 (scale, zero) per 128-group.
+ * Replaces: scatter_pack_rows(x, slots, codes_buf, params_buf, group_size,
+ *   lloyd_max, bits=2, quantizer_params=None)
+ *   (deployment/patches/rolaq_sglang.patch:9-34; codec of
+ *   mla_quant/oscar.py:120-144).
+ * x: fp32 [n, D] with row stride x_stride; slots: int32 [n].
+ * gain is the Lloyd stretch g; scale = fp32(span/3 * g) * std.
+ * n == 0 is a no-op. D must be 256 or 512, group_size 128.
+ */
+int rolaq_scatter_pack_rows(const float* x, int64_t x_stride, const int32_t* slots, int64_t n,
+                            int D, int group_size, float threshold, double gain,
+                            uint8_t* codes, float* params, void* stream);
+
+/*
+ * Fused cache writer: rotate each latent row by the layer's rotation on bf16
+ * MFMA (FP32 accumulate), quantize + pack it, and store the BF16 rope key,
+ * the BF16 rotated row of sink/recent tokens and the ring ownership maps.
+ * Replaces: try_fast_decode_store(pool, layer_id, loc, c_kv, k_pe) ->
+ *   _pack_and_aux (deployment/sglang/QuantKernel/mla_fused_writer.py:16-51,
+ *   54-107, 110-224), generalised to prefill chunks (positions given).
+ * latent: bf16 [n, D] (row stride latent_stride); k_pe: bf16 [n, R] with
+ * strides (pe_stride0, pe_stride1); rotation_t: bf16 [D, D] holding the
+ * transpose of R_eff = bf16(R) (row j = column j of R), or NULL for an
+ * un-rotated layer. loc/seq_lens/req_idx: int64 [n]; positions: int64 [n] or
+ * NULL (then position = seq_len - 1, a decode step). A row keeps a ring row
+ * iff (pos < P or pos >= seq_len - W) and 0 <= req < max_reqs and slot > 0.
+ * Rows with slot 0 (graph padding) write codes/params only.
+ */
+int rolaq_write_rows(const void* latent, int64_t latent_stride, const void* k_pe,
+                     int64_t pe_stride0, int64_t pe_stride1, const void* rotation_t,
+                     const int64_t* loc, const int64_t* seq_lens, const int64_t* positions,
+                     const int64_t* req_idx, int64_t n, int D, int R, int P, int W, int max_reqs,
+                     float threshold, double gain, uint8_t* codes, float* params, void* rope_buf,
+                     void* hp_c, int32_t* row_of_slot, int32_t* owner_of_row, void* stream);
+
+/*
+ * quant[i] = max(splits[i] - 1, 1); merge[i] = quant[i] + 1 (one launch).
+ * Replaces: prepare_gf_splits(splits, quant, merge)
+ *   (deployment/patches/rolaq_sglang.patch:81-92). int32 [n] each.
+ */
+int rolaq_prepare_gf_splits(const int32_t* splits, int32_t* quant, int32_t* merge, int64_t n,
+                            void* stream);
+
+/*
+ * Absorbed MLA decode attention over the packed cache, split-K + LSE merge.
+ * Replaces: packed_mla_decode_gf_fwd(q, ..., pool, max_kv_splits, attn_logits,
+ *   attn_lse, ...) with its quantized stage 1, _fwd_hp_window_stage1 and the
+ *   stage-2 merge (call site deployment/patches/rolaq_sglang.patch:51-111).
+ * q: bf16 [B, H, D + R] = (q_lat | q_rope), strides (q_stride_b, q_stride_h).
+ * Token t of request b lives in slot
+ *   kv_indices[kv_indptr[b] + t / page_size] * page_size + t % page_size
+ * (page_size a power of two; 1 = SGLang's token-level kv_indices).
+ * seq_lens: int64 [B] or NULL (then L_b = kv_indptr[b+1] - kv_indptr[b],
+ * page_size must be 1). req_idx: int64 [B] ring-row request index.
+ * num_kv_splits: int32 [B] requested splits ns_b (1 <= ns_b <= max_kv_splits);
+ * positions P <= t < L_b - W are split over max(ns_b - 1, 1) INT2 splits,
+ * the window rows (t < P or t >= L_b - W, read from hp_c) form split
+ * max(ns_b - 1, 1). Partials (normalised output, natural-log LSE; empty
+ * splits 0 / -1e4) go to attn_logits fp32 [B, H, max_kv_splits + 1, D] and
+ * attn_lse fp32 [B, H, max_kv_splits + 1]; the merged output to out: bf16
+ * [B, H, D] with strides (out_stride_b, out_stride_h), in the rotated frame.
+ * Supported shapes: (D, R, H) with D = 512, R = 64, H <= 16 or D = 256, R = 32,
+ * H <= 16 or 33 <= H <= 48.
+ */
+int rolaq_decode_fwd(const void* q, int64_t q_stride_b, int64_t q_stride_h, const uint8_t* codes,
+                     const float* params, const void* rope_buf, const void* hp_c,
+                     const int32_t* kv_indptr, const int32_t* kv_indices, int page_size,
+                     const int64_t* seq_lens, const int64_t* req_idx,
+                     const int32_t* num_kv_splits, int max_kv_splits, int B, int H, int D, int R,
+                     int P, int W, float sm_scale, float* attn_logits, float* attn_lse,
+                     void* out, int64_t out_stride_b, int64_t out_stride_h, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* ROLAQ_MLA_H */

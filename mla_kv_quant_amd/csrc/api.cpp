@@ -1,0 +1,202 @@
+// C ABI of the packed-INT2 RoLaQ MLA path (declarations: include/rolaq_mla.h).
+// Validates every argument on the host before any launch; allocates nothing.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+
+#include "../../include/rolaq_mla.h"
+
+#include "rolaq_args.h"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int hip_status(hipError_t e, const char* what) {
+  if (e != hipSuccess) return fail(ROLAQ_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+  g_err[0] = '\0';
+  return ROLAQ_OK;
+}
+
+bool aligned(const void* p, size_t a) { return (reinterpret_cast<uintptr_t>(p) % a) == 0; }
+
+// The Lloyd scale constant: span / 3 * gain in float64, then cast to FP32
+// (mla_quant/oscar.py:141-142 multiplies a Python float by an FP32 tensor).
+float lloyd_kscale(double gain) {
+  const double c0 = -1.5095585584640503, c3 = 1.5095585584640503;
+  return static_cast<float>((c3 - c0) / 3.0 * gain);
+}
+
+bool good_params(float thr, double gain) {
+  return std::isfinite(thr) && std::isfinite(gain) && thr > 0.f && gain > 0.0;
+}
+
+int cu_count() {
+  static thread_local int dev = -1, cus = 0;
+  int d = 0;
+  if (hipGetDevice(&d) != hipSuccess) return 256;
+  if (d != dev) {
+    int c = 0;
+    if (hipDeviceGetAttribute(&c, hipDeviceAttributeMultiprocessorCount, d) != hipSuccess || c <= 0) c = 256;
+    dev = d;
+    cus = c;
+  }
+  return cus;
+}
+
+}  // namespace
+
+extern "C" {
+
+const char* rolaq_last_error(void) { return g_err; }
+
+int rolaq_abi_version(void) { return 1; }
+
+int rolaq_scatter_pack_rows(const float* x, int64_t x_stride, const int32_t* slots, int64_t n, int D,
+                            int group_size, float threshold, double gain, uint8_t* codes, float* params,
+                            void* stream) {
+  if (n < 0) return fail(ROLAQ_ERR_INVALID, "scatter_pack_rows: n < 0");
+  if (n == 0) { g_err[0] = '\0'; return ROLAQ_OK; }
+  if (group_size != 128) return fail(ROLAQ_ERR_INVALID, "scatter_pack_rows: group_size must be 128");
+  if (D != 512 && D != 256) return fail(ROLAQ_ERR_INVALID, "scatter_pack_rows: D must be 256 or 512, got %d", D);
+  if (!x || !slots || !codes || !params) return fail(ROLAQ_ERR_INVALID, "scatter_pack_rows: null pointer");
+  if (x_stride < D || x_stride % 4 || !aligned(x, 16))
+    return fail(ROLAQ_ERR_INVALID, "scatter_pack_rows: x must be 16-byte aligned with a row stride >= D, multiple of 4");
+  if (!good_params(threshold, gain)) return fail(ROLAQ_ERR_INVALID, "scatter_pack_rows: invalid threshold/gain");
+  if (!aligned(codes, 4) || !aligned(params, 8)) return fail(ROLAQ_ERR_INVALID, "scatter_pack_rows: misaligned cache buffers");
+  return hip_status(rolaq_launch_pack_f32(x, x_stride, slots, n, D, threshold, lloyd_kscale(gain), codes, params,
+                                          static_cast<hipStream_t>(stream)),
+                    "scatter_pack_rows launch");
+}
+
+int rolaq_write_rows(const void* latent, int64_t latent_stride, const void* k_pe, int64_t pe_stride0,
+                     int64_t pe_stride1, const void* rotation_t, const int64_t* loc, const int64_t* seq_lens,
+                     const int64_t* positions, const int64_t* req_idx, int64_t n, int D, int R, int P, int W,
+                     int max_reqs, float threshold, double gain, uint8_t* codes, float* params, void* rope_buf,
+                     void* hp_c, int32_t* row_of_slot, int32_t* owner_of_row, void* stream) {
+  if (n < 0) return fail(ROLAQ_ERR_INVALID, "write_rows: n < 0");
+  if (n == 0) { g_err[0] = '\0'; return ROLAQ_OK; }
+  if (!((D == 512 && R == 64) || (D == 256 && R == 32)))
+    return fail(ROLAQ_ERR_INVALID, "write_rows: (D, R) must be (512, 64) or (256, 32), got (%d, %d)", D, R);
+  if (!latent || !k_pe || !loc || !seq_lens || !req_idx || !codes || !params || !rope_buf || !hp_c ||
+      !row_of_slot || !owner_of_row)
+    return fail(ROLAQ_ERR_INVALID, "write_rows: null pointer");
+  if (latent_stride < D || latent_stride % 8 || !aligned(latent, 16))
+    return fail(ROLAQ_ERR_INVALID, "write_rows: latent must be 16-byte aligned with a row stride >= D, multiple of 8");
+  if (rotation_t && !aligned(rotation_t, 16)) return fail(ROLAQ_ERR_INVALID, "write_rows: rotation must be 16-byte aligned");
+  if (P < 0 || W < 0 || max_reqs < 0) return fail(ROLAQ_ERR_INVALID, "write_rows: negative window or max_reqs");
+  if (!good_params(threshold, gain)) return fail(ROLAQ_ERR_INVALID, "write_rows: invalid threshold/gain");
+  if (!aligned(codes, 4) || !aligned(params, 8) || !aligned(hp_c, 8))
+    return fail(ROLAQ_ERR_INVALID, "write_rows: misaligned cache buffers");
+  const float ks = lloyd_kscale(gain);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (!rotation_t) {
+    rolaq::AuxArgs aux{static_cast<const uint16_t*>(k_pe), pe_stride0, pe_stride1, seq_lens, positions, req_idx,
+                       R, P, W, max_reqs, static_cast<uint16_t*>(rope_buf), static_cast<uint16_t*>(hp_c),
+                       row_of_slot, owner_of_row};
+    return hip_status(rolaq_launch_pack_bf16_aux(static_cast<const uint16_t*>(latent), latent_stride, loc, n, D,
+                                                 threshold, ks, codes, params, aux, s),
+                      "write_rows (un-rotated) launch");
+  }
+  rolaq::WriterArgs a{};
+  a.x = static_cast<const uint16_t*>(latent);
+  a.xs = latent_stride;
+  a.rt = static_cast<const uint16_t*>(rotation_t);
+  a.loc = loc;
+  a.n = n;
+  a.thr = threshold;
+  a.kscale = ks;
+  a.codes = codes;
+  a.params = params;
+  a.k_pe = static_cast<const uint16_t*>(k_pe);
+  a.pe_s0 = pe_stride0;
+  a.pe_s1 = pe_stride1;
+  a.seq_lens = seq_lens;
+  a.positions = positions;
+  a.req_idx = req_idx;
+  a.R = R;
+  a.P = P;
+  a.W = W;
+  a.max_reqs = max_reqs;
+  a.rope = static_cast<uint16_t*>(rope_buf);
+  a.hp = static_cast<uint16_t*>(hp_c);
+  a.row_of_slot = row_of_slot;
+  a.owner_of_row = owner_of_row;
+  return hip_status(rolaq_launch_writer(a, D, cu_count(), s), "write_rows launch");
+}
+
+int rolaq_prepare_gf_splits(const int32_t* splits, int32_t* quant, int32_t* merge, int64_t n, void* stream) {
+  if (n < 0) return fail(ROLAQ_ERR_INVALID, "prepare_gf_splits: n < 0");
+  if (n == 0) { g_err[0] = '\0'; return ROLAQ_OK; }
+  if (!splits || !quant || !merge) return fail(ROLAQ_ERR_INVALID, "prepare_gf_splits: null pointer");
+  return hip_status(rolaq_launch_prepare_splits(splits, quant, merge, n, static_cast<hipStream_t>(stream)),
+                    "prepare_gf_splits launch");
+}
+
+int rolaq_decode_fwd(const void* q, int64_t q_stride_b, int64_t q_stride_h, const uint8_t* codes,
+                     const float* params, const void* rope_buf, const void* hp_c, const int32_t* kv_indptr,
+                     const int32_t* kv_indices, int page_size, const int64_t* seq_lens, const int64_t* req_idx,
+                     const int32_t* num_kv_splits, int max_kv_splits, int B, int H, int D, int R, int P, int W,
+                     float sm_scale, float* attn_logits, float* attn_lse, void* out, int64_t out_stride_b,
+                     int64_t out_stride_h, void* stream) {
+  if (B < 0) return fail(ROLAQ_ERR_INVALID, "decode_fwd: B < 0");
+  if (B == 0) { g_err[0] = '\0'; return ROLAQ_OK; }
+  if (!((D == 512 && R == 64) || (D == 256 && R == 32)))
+    return fail(ROLAQ_ERR_INVALID, "decode_fwd: (D, R) must be (512, 64) or (256, 32), got (%d, %d)", D, R);
+  const int nhb = (H + 15) / 16;
+  const bool shape_ok = (D == 512 && nhb == 1) || (D == 256 && (nhb == 1 || nhb == 3));
+  if (H <= 0 || !shape_ok) return fail(ROLAQ_ERR_INVALID, "decode_fwd: unsupported head count %d for D=%d", H, D);
+  if (!q || !codes || !params || !rope_buf || !hp_c || !kv_indptr || !kv_indices || !req_idx || !num_kv_splits ||
+      !attn_logits || !attn_lse || !out)
+    return fail(ROLAQ_ERR_INVALID, "decode_fwd: null pointer");
+  if (page_size < 1 || (page_size & (page_size - 1)))
+    return fail(ROLAQ_ERR_INVALID, "decode_fwd: page_size must be a power of two, got %d", page_size);
+  if (!seq_lens && page_size != 1) return fail(ROLAQ_ERR_INVALID, "decode_fwd: seq_lens required when page_size > 1");
+  if (max_kv_splits < 1 || max_kv_splits > 4096) return fail(ROLAQ_ERR_INVALID, "decode_fwd: max_kv_splits out of range");
+  if (P < 0 || W < 0 || P + W > 64) return fail(ROLAQ_ERR_INVALID, "decode_fwd: need 0 <= P, W and P + W <= 64");
+  if (!aligned(q, 16) || q_stride_b % 8 || q_stride_h % 8 || q_stride_h < D + R)
+    return fail(ROLAQ_ERR_INVALID, "decode_fwd: q must be 16-byte aligned with strides multiple of 8 and q_stride_h >= D+R");
+  if (!aligned(codes, 16) || !aligned(params, 16) || !aligned(rope_buf, 16) || !aligned(hp_c, 16))
+    return fail(ROLAQ_ERR_INVALID, "decode_fwd: cache buffers must be 16-byte aligned");
+  if (!(sm_scale > 0.f) || !std::isfinite(sm_scale)) return fail(ROLAQ_ERR_INVALID, "decode_fwd: invalid sm_scale");
+  int shift = 0;
+  while ((1 << shift) < page_size) ++shift;
+  rolaq::DecodeArgs a{};
+  a.q = static_cast<const uint16_t*>(q);
+  a.q_sb = q_stride_b;
+  a.q_sh = q_stride_h;
+  a.codes = codes;
+  a.params = params;
+  a.rope = static_cast<const uint16_t*>(rope_buf);
+  a.hp = static_cast<const uint16_t*>(hp_c);
+  a.kv_indptr = kv_indptr;
+  a.kv_indices = kv_indices;
+  a.page_shift = shift;
+  a.seq_lens = seq_lens;
+  a.req_idx = req_idx;
+  a.num_kv_splits = num_kv_splits;
+  a.S1 = max_kv_splits + 1;
+  a.B = B;
+  a.H = H;
+  a.P = P;
+  a.W = W;
+  a.sm_scale = sm_scale;
+  a.logits = attn_logits;
+  a.lse = attn_lse;
+  return hip_status(rolaq_launch_decode(a, D, R, max_kv_splits, static_cast<uint16_t*>(out), out_stride_b,
+                                        out_stride_h, static_cast<hipStream_t>(stream)),
+                    "decode_fwd launch");
+}
+
+}  // extern "C"

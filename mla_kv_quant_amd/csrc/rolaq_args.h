@@ -1,0 +1,76 @@
+// Kernel argument blocks shared by the host launchers and the C ABI layer.
+#pragma once
+
+#include <stdint.h>
+
+namespace rolaq {
+
+struct DecodeArgs {
+  const uint16_t* q;
+  int64_t q_sb, q_sh;
+  const uint8_t* codes;
+  const float* params;
+  const uint16_t* rope;
+  const uint16_t* hp;
+  const int32_t* kv_indptr;
+  const int32_t* kv_indices;
+  int page_shift;
+  const int64_t* seq_lens;
+  const int64_t* req_idx;
+  const int32_t* num_kv_splits;
+  int S1;  // max_kv_splits + 1
+  int B, H, P, W;
+  float sm_scale;
+  float* logits;  // [B, H, S1, D]
+  float* lse;     // [B, H, S1]
+};
+
+struct AuxArgs {
+  const uint16_t* k_pe;
+  int64_t pe_s0, pe_s1;
+  const int64_t* seq_lens;
+  const int64_t* positions;
+  const int64_t* req_idx;
+  int R, P, W, max_reqs;
+  uint16_t* rope;
+  uint16_t* hp;
+  int32_t* row_of_slot;
+  int32_t* owner_of_row;
+};
+
+struct WriterArgs {
+  const uint16_t* x;
+  int64_t xs;
+  const uint16_t* rt;  // R_eff^T [D, D] bf16
+  const int64_t* loc;
+  int64_t n;
+  float thr, kscale;
+  uint8_t* codes;
+  float* params;
+  const uint16_t* k_pe;
+  int64_t pe_s0, pe_s1;
+  const int64_t* seq_lens;
+  const int64_t* positions;
+  const int64_t* req_idx;
+  int R, P, W, max_reqs;
+  uint16_t* rope;
+  uint16_t* hp;
+  int32_t* row_of_slot;
+  int32_t* owner_of_row;
+  int nstripes;
+};
+
+}  // namespace rolaq
+
+// Host launchers (defined next to their kernels).
+#include <hip/hip_runtime.h>
+hipError_t rolaq_launch_decode(const rolaq::DecodeArgs& a, int D, int R, int max_splits, uint16_t* out,
+                               int64_t o_sb, int64_t o_sh, hipStream_t stream);
+hipError_t rolaq_launch_pack_f32(const float* x, int64_t xs, const int32_t* slots, int64_t n, int D,
+                                 float thr, float kscale, uint8_t* codes, float* params, hipStream_t stream);
+hipError_t rolaq_launch_pack_bf16_aux(const uint16_t* x, int64_t xs, const int64_t* loc, int64_t n, int D,
+                                      float thr, float kscale, uint8_t* codes, float* params,
+                                      const rolaq::AuxArgs& aux, hipStream_t stream);
+hipError_t rolaq_launch_prepare_splits(const int32_t* splits, int32_t* quant, int32_t* merge, int64_t n,
+                                       hipStream_t stream);
+hipError_t rolaq_launch_writer(const rolaq::WriterArgs& a, int D, int num_cus, hipStream_t stream);

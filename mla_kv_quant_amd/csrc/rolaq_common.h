@@ -1,0 +1,80 @@
+// Shared device helpers for the RoLaQ packed-INT2 MLA kernels (gfx950 only).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+namespace rolaq {
+
+constexpr int kGroup = 128;            // quantization group (elements)
+constexpr int kCodesPerWord = 16;      // 2-bit codes per 32-bit word
+constexpr float kZeroOffset = 1.5f;    // -C0 / (span / 3) of the Lloyd grid
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+constexpr float kNeutralLse = -1.0e4f;  // empty split (SGLang decode convention)
+
+// D = A(16x32) * B(32x16) + C on bf16 inputs, fp32 accumulate.
+// Lane l holds A[l%16][8(l/16)+i], B[8(l/16)+i][l%16] (i = 0..7, two per dword,
+// low half first) and C[4(l/16)+j][l%16] (j = 0..3).
+__device__ __forceinline__ f32x4 mfma16x16x32(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
+                                                 __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
+}
+
+// Two fp32 -> one dword of two bf16 (round to nearest even), low half = lo.
+__device__ __forceinline__ uint32_t pack_bf16(float lo, float hi) {
+  f32x2 f = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, bf16x2_t));
+}
+
+__device__ __forceinline__ float bf16_lo(uint32_t v) { return __uint_as_float(v << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t v) { return __uint_as_float(v & 0xffff0000u); }
+__device__ __forceinline__ float bf16_to_float(uint16_t v) { return __uint_as_float(uint32_t(v) << 16); }
+__device__ __forceinline__ uint16_t float_to_bf16(float f) {
+  return uint16_t(pack_bf16(f, 0.0f) & 0xffffu);
+}
+
+// In-place unpack of one packed word (16 codes; code p at bits 2p) into eight
+// dwords of two bf16 each. Dword k holds (code k, code k + 8) as the bf16
+// values 4 + c * 2^(e_k - 5), e = {0, 2, 4, 0, 2, 4, 0, 2}: the code bits are
+// masked straight into the mantissa of 4.0 (0x4080), so a dword costs one
+// and-or (plus a shared shift for k >= 3).
+__device__ __forceinline__ void unpack_word(uint32_t w, uint32_t d[8]) {
+  const uint32_t base = 0x40804080u;
+  d[0] = (w & 0x00030003u) | base;
+  d[1] = (w & 0x000C000Cu) | base;
+  d[2] = (w & 0x00300030u) | base;
+  const uint32_t w6 = w >> 6;
+  d[3] = (w6 & 0x00030003u) | base;
+  d[4] = (w6 & 0x000C000Cu) | base;
+  d[5] = (w6 & 0x00300030u) | base;
+  const uint32_t w12 = w >> 12;
+  d[6] = (w12 & 0x00030003u) | base;
+  d[7] = (w12 & 0x000C000Cu) | base;
+}
+
+// Mantissa shift e_k of pair k in unpack_word; the decoded value is
+// 4 + c * 2^(e_k - 5), so weights on pair k are scaled by 2^(5 - e_k).
+__host__ __device__ constexpr int pair_shift(int k) { return k < 3 ? 2 * k : (k < 6 ? 2 * k - 6 : 2 * k - 12); }
+__host__ __device__ constexpr float pair_weight(int k) { return float(1 << (5 - pair_shift(k))); }
+
+__device__ __forceinline__ float wave_max_over_groups(float v) {
+  // max over lanes l, l^16, l^32, l^48 (the four 16-lane rows of a wave)
+  v = fmaxf(v, __shfl_xor(v, 16));
+  v = fmaxf(v, __shfl_xor(v, 32));
+  return v;
+}
+__device__ __forceinline__ float wave_sum_over_groups(float v) {
+  v += __shfl_xor(v, 16);
+  v += __shfl_xor(v, 32);
+  return v;
+}
+
+}  // namespace rolaq

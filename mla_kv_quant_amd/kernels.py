@@ -1,0 +1,176 @@
+"""Tensor-level calls into the C ABI (``include/rolaq_mla.h``).
+
+Each function checks devices, dtypes and layouts on the host, then passes raw
+pointers and the current HIP stream of the tensors' device. No allocation,
+no synchronisation, no host branch on device data.
+"""
+
+from __future__ import annotations
+
+import ctypes
+
+import torch
+
+from . import _lib
+
+GROUP_SIZE = 128
+
+
+def _p(t: torch.Tensor | None):
+    return ctypes.c_void_p(t.data_ptr()) if t is not None else ctypes.c_void_p(0)
+
+
+def _stream(t: torch.Tensor):
+    return ctypes.c_void_p(torch.cuda.current_stream(t.device).cuda_stream)
+
+
+def _need(t: torch.Tensor, name: str, dtype: torch.dtype, device: torch.device, ndim: int | None = None):
+    if not isinstance(t, torch.Tensor):
+        raise TypeError(f"{name} must be a tensor")
+    if t.dtype != dtype:
+        raise TypeError(f"{name} must be {dtype}, got {t.dtype}")
+    if t.device != device:
+        raise ValueError(f"{name} must be on {device}, got {t.device}")
+    if ndim is not None and t.dim() != ndim:
+        raise ValueError(f"{name} must have {ndim} dims, got {tuple(t.shape)}")
+
+
+def _contig(t: torch.Tensor, name: str):
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+
+
+def scatter_pack_rows(x: torch.Tensor, slots: torch.Tensor, codes: torch.Tensor, params: torch.Tensor,
+                      threshold: float, gain: float) -> None:
+    """Quantize FP32 rotated rows ``x [n, D]`` into ``codes``/``params`` at ``slots``."""
+    dev = x.device
+    _need(x, "x", torch.float32, dev, 2)
+    n, D = x.shape
+    _need(slots, "slots", torch.int32, dev, 1)
+    _need(codes, "codes", torch.uint8, dev, 2)
+    _need(params, "params", torch.float32, dev, 3)
+    if slots.numel() != n or codes.shape[1] != D // 4 or tuple(params.shape[1:]) != (D // GROUP_SIZE, 2):
+        raise ValueError("scatter_pack_rows: shape mismatch")
+    if x.stride(1) != 1:
+        raise ValueError("x rows must be contiguous")
+    _contig(slots, "slots"), _contig(codes, "codes"), _contig(params, "params")
+    _lib.check(_lib.load().rolaq_scatter_pack_rows(
+        _p(x), x.stride(0), _p(slots), n, D, GROUP_SIZE, float(threshold), float(gain),
+        _p(codes), _p(params), _stream(x)))
+
+
+def write_rows(latent: torch.Tensor, k_pe: torch.Tensor, rotation_t: torch.Tensor | None,
+               loc: torch.Tensor, seq_lens: torch.Tensor, positions: torch.Tensor | None,
+               req_idx: torch.Tensor, codes: torch.Tensor, params: torch.Tensor,
+               rope_buf: torch.Tensor, hp_c: torch.Tensor, row_of_slot: torch.Tensor,
+               owner_of_row: torch.Tensor, P: int, W: int, max_reqs: int,
+               threshold: float, gain: float) -> None:
+    """Fused rotate + quantize + pack + rope/window stores for ``n`` rows."""
+    dev = latent.device
+    _need(latent, "latent", torch.bfloat16, dev, 2)
+    n, D = latent.shape
+    _need(k_pe, "k_pe", torch.bfloat16, dev, 2)
+    R = k_pe.shape[1]
+    if k_pe.shape[0] != n:
+        raise ValueError("k_pe rows must match latent rows")
+    if rotation_t is not None:
+        _need(rotation_t, "rotation_t", torch.bfloat16, dev, 2)
+        _contig(rotation_t, "rotation_t")
+        if tuple(rotation_t.shape) != (D, D):
+            raise ValueError("rotation_t must be [D, D]")
+    for name, t in (("loc", loc), ("seq_lens", seq_lens), ("req_idx", req_idx)):
+        _need(t, name, torch.int64, dev, 1)
+        _contig(t, name)
+        if t.numel() != n:
+            raise ValueError(f"{name} must have {n} entries")
+    if positions is not None:
+        _need(positions, "positions", torch.int64, dev, 1)
+        _contig(positions, "positions")
+        if positions.numel() != n:
+            raise ValueError("positions must have n entries")
+    _need(codes, "codes", torch.uint8, dev, 2)
+    _need(params, "params", torch.float32, dev, 3)
+    _need(rope_buf, "rope_buf", torch.bfloat16, dev, 2)
+    _need(hp_c, "hp_c", torch.bfloat16, dev, 2)
+    _need(row_of_slot, "row_of_slot", torch.int32, dev, 1)
+    _need(owner_of_row, "owner_of_row", torch.int32, dev, 1)
+    for name, t in (("codes", codes), ("params", params), ("rope_buf", rope_buf), ("hp_c", hp_c),
+                    ("row_of_slot", row_of_slot), ("owner_of_row", owner_of_row)):
+        _contig(t, name)
+    if codes.shape[1] != D // 4 or tuple(params.shape[1:]) != (D // GROUP_SIZE, 2) or rope_buf.shape[1] != R \
+            or hp_c.shape[1] != D:
+        raise ValueError("cache buffers do not match (D, R)")
+    if hp_c.shape[0] < 1 + max_reqs * (P + W) or owner_of_row.shape[0] < 1 + max_reqs * (P + W):
+        raise ValueError("hp_c / owner_of_row are smaller than 1 + max_reqs * (P + W)")
+    if latent.stride(1) != 1:
+        raise ValueError("latent rows must be contiguous")
+    _lib.check(_lib.load().rolaq_write_rows(
+        _p(latent), latent.stride(0), _p(k_pe), k_pe.stride(0), k_pe.stride(1), _p(rotation_t),
+        _p(loc), _p(seq_lens), _p(positions), _p(req_idx), n, D, R, int(P), int(W), int(max_reqs),
+        float(threshold), float(gain), _p(codes), _p(params), _p(rope_buf), _p(hp_c),
+        _p(row_of_slot), _p(owner_of_row), _stream(latent)))
+
+
+def prepare_gf_splits(splits: torch.Tensor, quant: torch.Tensor, merge: torch.Tensor) -> None:
+    """``quant = max(splits - 1, 1)``, ``merge = quant + 1`` in one launch."""
+    dev = splits.device
+    for name, t in (("splits", splits), ("quant", quant), ("merge", merge)):
+        _need(t, name, torch.int32, dev)
+        _contig(t, name)
+        if t.numel() != splits.numel():
+            raise ValueError("splits/quant/merge must have the same size")
+    _lib.check(_lib.load().rolaq_prepare_gf_splits(_p(splits), _p(quant), _p(merge), splits.numel(),
+                                                   _stream(splits)))
+
+
+def decode_fwd(q: torch.Tensor, codes: torch.Tensor, params: torch.Tensor, rope_buf: torch.Tensor,
+               hp_c: torch.Tensor, kv_indptr: torch.Tensor, kv_indices: torch.Tensor,
+               seq_lens: torch.Tensor | None, req_idx: torch.Tensor, num_kv_splits: torch.Tensor,
+               max_kv_splits: int, attn_logits: torch.Tensor, attn_lse: torch.Tensor,
+               out: torch.Tensor, sm_scale: float, P: int, W: int, page_size: int = 1) -> torch.Tensor:
+    """Absorbed decode over the packed cache: ``q [B, H, D+R]`` -> ``out [B, H, D]``."""
+    dev = q.device
+    _need(q, "q", torch.bfloat16, dev, 3)
+    B, H, DR = q.shape
+    D = codes.shape[1] * 4
+    R = DR - D
+    if q.stride(2) != 1:
+        raise ValueError("q must be contiguous in its last dim")
+    _need(codes, "codes", torch.uint8, dev, 2)
+    _need(params, "params", torch.float32, dev, 3)
+    _need(rope_buf, "rope_buf", torch.bfloat16, dev, 2)
+    _need(hp_c, "hp_c", torch.bfloat16, dev, 2)
+    for name, t in (("codes", codes), ("params", params), ("rope_buf", rope_buf), ("hp_c", hp_c)):
+        _contig(t, name)
+    if rope_buf.shape[1] != R or hp_c.shape[1] != D or tuple(params.shape[1:]) != (D // GROUP_SIZE, 2):
+        raise ValueError("cache buffers do not match q's (D, R)")
+    _need(kv_indptr, "kv_indptr", torch.int32, dev, 1)
+    _need(kv_indices, "kv_indices", torch.int32, dev, 1)
+    _need(req_idx, "req_idx", torch.int64, dev, 1)
+    _need(num_kv_splits, "num_kv_splits", torch.int32, dev, 1)
+    for name, t in (("kv_indptr", kv_indptr), ("kv_indices", kv_indices), ("req_idx", req_idx),
+                    ("num_kv_splits", num_kv_splits)):
+        _contig(t, name)
+    if kv_indptr.numel() < B + 1 or req_idx.numel() < B or num_kv_splits.numel() < B:
+        raise ValueError("index tensors are shorter than the batch")
+    if seq_lens is not None:
+        _need(seq_lens, "seq_lens", torch.int64, dev, 1)
+        _contig(seq_lens, "seq_lens")
+        if seq_lens.numel() < B:
+            raise ValueError("seq_lens is shorter than the batch")
+    S1 = int(max_kv_splits) + 1
+    _need(attn_logits, "attn_logits", torch.float32, dev)
+    _need(attn_lse, "attn_lse", torch.float32, dev)
+    _contig(attn_logits, "attn_logits"), _contig(attn_lse, "attn_lse")
+    if tuple(attn_logits.shape[1:]) != (H, S1, D) or attn_logits.shape[0] < B \
+            or tuple(attn_lse.shape[1:]) != (H, S1) or attn_lse.shape[0] < B:
+        raise ValueError("attn_logits / attn_lse must be [>=B, H, max_kv_splits + 1, (D)]")
+    _need(out, "out", torch.bfloat16, dev, 3)
+    if tuple(out.shape) != (B, H, D) or out.stride(2) != 1:
+        raise ValueError("out must be [B, H, D] with a contiguous last dim")
+    _lib.check(_lib.load().rolaq_decode_fwd(
+        _p(q), q.stride(0), q.stride(1), _p(codes), _p(params), _p(rope_buf), _p(hp_c),
+        _p(kv_indptr), _p(kv_indices), int(page_size), _p(seq_lens), _p(req_idx), _p(num_kv_splits),
+        int(max_kv_splits), B, H, D, R, int(P), int(W), float(sm_scale), _p(attn_logits),
+        _p(attn_lse), _p(out), out.stride(0), out.stride(1), _stream(q)))
+    return out

@@ -1,0 +1,64 @@
+"""C-ABI library: loads, exports every declared symbol, rejects bad arguments (CPU only)."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from mla_kv_quant_amd import _lib
+
+ROOT = Path(__file__).resolve().parents[1]
+
+
+def declared_symbols():
+    text = (ROOT / "include" / "rolaq_mla.h").read_text()
+    return sorted(set(re.findall(r"^\s*(?:const\s+char\s*\*|int)\s+(rolaq_\w+)\s*\(", text, re.M)))
+
+
+def test_header_declares_the_entry_points():
+    syms = declared_symbols()
+    for name in ("rolaq_last_error", "rolaq_abi_version", "rolaq_scatter_pack_rows", "rolaq_write_rows",
+                 "rolaq_prepare_gf_splits", "rolaq_decode_fwd"):
+        assert name in syms
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    for name in declared_symbols():
+        assert hasattr(lib, name), name
+    # every declared symbol has a ctypes signature in the binding
+    assert set(declared_symbols()) - {"rolaq_last_error"} <= set(_lib.SIGNATURES)
+    assert lib.rolaq_abi_version() == 1
+
+
+def test_invalid_arguments_are_rejected_before_any_launch():
+    lib = _lib.load()
+    assert lib.rolaq_prepare_gf_splits(None, None, None, 4, None) == _lib.ROLAQ_ERR_INVALID
+    assert b"null pointer" in lib.rolaq_last_error()
+    # n == 0 is a no-op even with null pointers
+    assert lib.rolaq_prepare_gf_splits(None, None, None, 0, None) == _lib.ROLAQ_OK
+    assert lib.rolaq_scatter_pack_rows(None, 512, None, 0, 512, 128, 0.98, 1.16, None, None, None) == 0
+    bad = lib.rolaq_scatter_pack_rows(ctypes.c_void_p(16), 512, ctypes.c_void_p(16), 4, 384, 128,
+                                      0.98, 1.16, ctypes.c_void_p(16), ctypes.c_void_p(16), None)
+    assert bad == _lib.ROLAQ_ERR_INVALID and b"D must be" in lib.rolaq_last_error()
+    bad = lib.rolaq_scatter_pack_rows(ctypes.c_void_p(16), 512, ctypes.c_void_p(16), 4, 512, 64,
+                                      0.98, 1.16, ctypes.c_void_p(16), ctypes.c_void_p(16), None)
+    assert bad == _lib.ROLAQ_ERR_INVALID and b"group_size" in lib.rolaq_last_error()
+    bad = lib.rolaq_scatter_pack_rows(ctypes.c_void_p(16), 512, ctypes.c_void_p(16), 4, 512, 128,
+                                      float("nan"), 1.16, ctypes.c_void_p(16), ctypes.c_void_p(16), None)
+    assert bad == _lib.ROLAQ_ERR_INVALID
+    p = ctypes.c_void_p(256)
+    args = [p, 16 * 576, 576, p, p, p, p, p, p, 3, p, p, p, 8, 4, 16, 512, 64, 4, 16, 0.07, p, p, p, 8192, 512, None]
+    assert lib.rolaq_decode_fwd(*args) == _lib.ROLAQ_ERR_INVALID  # page_size 3
+    assert b"power of two" in lib.rolaq_last_error()
+    args[9] = 1
+    args[15] = 24  # H = 24 with D = 512 is not instantiated
+    assert lib.rolaq_decode_fwd(*args) == _lib.ROLAQ_ERR_INVALID
+
+
+def test_check_raises_value_error():
+    lib = _lib.load()
+    rc = lib.rolaq_prepare_gf_splits(None, None, None, 4, None)
+    with pytest.raises(ValueError):
+        _lib.check(rc)
