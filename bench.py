@@ -1,0 +1,330 @@
+"""Benchmark of the packed-INT2 RoLaQ MLA path on one MI355X.
+
+Headline (``value``): absorbed MLA decode attention over the INT2 cache at
+BASELINE config 2 -- batch 32 x 16384 context, 16 heads, latent 512, rope 64,
+s4r16 BF16 window, page 64 -- in microseconds per layer. A step is one decode
+pass over 27 layers, each with its own cache buffers (every layer's ~151 MB
+working set, so the 256 MB MALL cannot serve repeats). The cache is written
+beforehand by this library's fused writer from synthetic latents (N(0,1), 1%
+outlier channels x20, seeded rotation per layer).
+
+Also reported (``writer``): the fused cache writer at config 1 -- 64 sequences
+x 2048-token prefill chunk, 27 layers with their own buffers -- in Mtokens/s
+(token-layers per second) and as a fraction of HBM peak.
+
+``roofline``: algorithmic bytes per decode layer (288 B per INT2 token, window
+rows, q and out) over the measured layer time, against 8 TB/s. ``traffic`` is
+taken from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary when present.
+``cpu_baseline``: the oracle's dequantize-then-attention on the host cores for a
+bounded sample of config-2 sequences, scaled to one layer.
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import sys
+import time
+from pathlib import Path
+
+import numpy as np
+import torch
+
+ROOT = Path(__file__).resolve().parent
+sys.path.insert(0, str(ROOT))
+
+HBM_PEAK_GBS = 8000.0
+MFMA_BF16_PEAK_TFLOPS = 2500.0
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=3)
+    ap.add_argument("--layers", type=int, default=27)
+    ap.add_argument("--splits", type=int, default=0, help="num_kv_splits per request (0 = pick the fastest)")
+    ap.add_argument("--no-writer", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true")
+    return ap.parse_args()
+
+
+# ---------------------------------------------------------------------------
+# config 2: decode
+# ---------------------------------------------------------------------------
+class DecodeBench:
+    B, L, H, D, R, P, W, PAGE = 32, 16384, 16, 512, 64, 4, 16, 64
+
+    def __init__(self, layers: int, dev: str):
+        from mla_kv_quant_amd import kernels, synth
+
+        self.layers, self.dev = layers, dev
+        B, L, D, R, P, W, PAGE = self.B, self.L, self.D, self.R, self.P, self.W, self.PAGE
+        pages_per_seq = L // PAGE
+        npages = B * pages_per_seq
+        rng = np.random.default_rng(0)
+        perm = rng.permutation(np.arange(1, npages + 1)).astype(np.int64)  # page 0 = padding
+        page_table = perm.reshape(B, pages_per_seq)
+        self.num_slots = (npages + 1) * PAGE
+        self.kv_indptr = torch.arange(0, B * pages_per_seq + 1, pages_per_seq, dtype=torch.int32, device=dev)
+        self.kv_indices = torch.from_numpy(page_table.reshape(-1).astype(np.int32)).to(dev)
+        self.seq_lens = torch.full((B,), L, dtype=torch.int64, device=dev)
+        self.req = torch.arange(1, B + 1, dtype=torch.int64, device=dev)
+        slots = (torch.from_numpy(page_table).to(dev)[:, :, None] * PAGE
+                 + torch.arange(PAGE, device=dev)[None, None, :]).reshape(B, L)
+        positions = torch.arange(L, device=dev).repeat(B)
+        seqs = torch.full((B * L,), L, dtype=torch.int64, device=dev)
+        reqs = self.req.repeat_interleave(L)
+        loc = slots.reshape(-1).contiguous()
+        max_reqs = B + 1
+        hp_rows = 1 + max_reqs * (P + W)
+        self.caches = []
+        self.sm_scale = 1.0 / math.sqrt(192)
+        sigma = 2.0 / (self.sm_scale * math.sqrt(D + R))
+        for layer in range(layers):
+            c = {
+                "codes": torch.zeros(self.num_slots, D // 4, dtype=torch.uint8, device=dev),
+                "params": torch.zeros(self.num_slots, D // 128, 2, dtype=torch.float32, device=dev),
+                "rope": torch.zeros(self.num_slots, R, dtype=torch.bfloat16, device=dev),
+                "hp": torch.zeros(hp_rows, D, dtype=torch.bfloat16, device=dev),
+                "row": torch.full((self.num_slots,), -1, dtype=torch.int32, device=dev),
+                "owner": torch.zeros(hp_rows, dtype=torch.int32, device=dev),
+            }
+            rt = synth.layer_rotation(D, layer).to(torch.bfloat16).t().contiguous().to(dev)
+            x = synth.make_latent(B * L, D, max(1, D // 100), seed=10_000 + layer, device=dev)
+            pe = synth.make_normal((B * L, R), 20_000 + layer, device=dev)
+            kernels.write_rows(x, pe, rt, loc, seqs, positions, reqs, c["codes"], c["params"], c["rope"],
+                               c["hp"], c["row"], c["owner"], P, W, max_reqs,
+                               synth.DEFAULT_THRESHOLD, synth.DEFAULT_GAIN)
+            del x, pe
+            c["q"] = synth.make_normal((B, self.H, D + R), 30_000 + layer, std=sigma, device=dev)
+            self.caches.append(c)
+        torch.cuda.synchronize()
+        self.out = torch.empty(B, self.H, D, dtype=torch.bfloat16, device=dev)
+
+    def alloc_scratch(self, max_splits: int):
+        self.max_splits = max_splits
+        self.logits = torch.empty(self.B, self.H, max_splits + 1, self.D, device=self.dev)
+        self.lse = torch.empty(self.B, self.H, max_splits + 1, device=self.dev)
+
+    def set_splits(self, ns: int):
+        self.ns = torch.full((self.B,), ns, dtype=torch.int32, device=self.dev)
+
+    def step(self):
+        from mla_kv_quant_amd import kernels
+
+        for c in self.caches:
+            kernels.decode_fwd(c["q"], c["codes"], c["params"], c["rope"], c["hp"], self.kv_indptr,
+                               self.kv_indices, self.seq_lens, self.req, self.ns, self.max_splits,
+                               self.logits, self.lse, self.out, self.sm_scale, self.P, self.W, self.PAGE)
+
+    def bytes_per_layer(self) -> float:
+        B, L, P, W, D, R, H = self.B, self.L, self.P, self.W, self.D, self.R, self.H
+        int2 = B * (L - P - W) * (D // 4 + 8 * (D // 128) + 2 * R)
+        window = B * (P + W) * (2 * D + 2 * R)
+        q_out = B * H * (D + R) * 2 + B * H * D * 2
+        return float(int2 + window + q_out)
+
+    def flops_per_layer(self) -> float:
+        return float(2 * self.B * self.L * self.H * (2 * self.D + self.R))
+
+
+def time_loop(fn, steps: int, warmup: int) -> float:
+    """Milliseconds per step: events on the current stream around exactly ``steps`` steps."""
+    for _ in range(warmup):
+        fn()
+    torch.cuda.synchronize()
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for _ in range(steps):
+        fn()
+    end.record()
+    torch.cuda.synchronize()
+    return start.elapsed_time(end) / steps
+
+
+# ---------------------------------------------------------------------------
+# config 1: writer
+# ---------------------------------------------------------------------------
+class WriterBench:
+    SEQS, CHUNK, D, R, P, W, PAGE = 64, 2048, 512, 64, 4, 16, 64
+
+    def __init__(self, layers: int, dev: str):
+        from mla_kv_quant_amd import synth
+
+        self.layers, self.dev = layers, dev
+        S, C, D, R, P, W, PAGE = self.SEQS, self.CHUNK, self.D, self.R, self.P, self.W, self.PAGE
+        n = S * C
+        self.n = n
+        pages = np.random.default_rng(1).permutation(np.arange(1, S * (C // PAGE) + 1)).reshape(S, C // PAGE)
+        slots = (torch.from_numpy(pages).to(dev)[:, :, None] * PAGE + torch.arange(PAGE, device=dev)).reshape(-1)
+        self.loc = slots.contiguous()
+        self.positions = torch.arange(C, device=dev).repeat(S)
+        self.seqs = torch.full((n,), C, dtype=torch.int64, device=dev)
+        self.reqs = torch.arange(1, S + 1, dtype=torch.int64, device=dev).repeat_interleave(C)
+        self.max_reqs = S + 1
+        num_slots = (S * (C // PAGE) + 1) * PAGE
+        hp_rows = 1 + self.max_reqs * (P + W)
+        self.layers_data = []
+        for layer in range(layers):
+            self.layers_data.append({
+                "x": synth.make_latent(n, D, max(1, D // 100), seed=40_000 + layer, device=dev),
+                "pe": synth.make_normal((n, R), 50_000 + layer, device=dev),
+                "rt": synth.layer_rotation(D, layer).to(torch.bfloat16).t().contiguous().to(dev),
+                "codes": torch.zeros(num_slots, D // 4, dtype=torch.uint8, device=dev),
+                "params": torch.zeros(num_slots, D // 128, 2, dtype=torch.float32, device=dev),
+                "rope": torch.zeros(num_slots, R, dtype=torch.bfloat16, device=dev),
+                "hp": torch.zeros(hp_rows, D, dtype=torch.bfloat16, device=dev),
+                "row": torch.full((num_slots,), -1, dtype=torch.int32, device=dev),
+                "owner": torch.zeros(hp_rows, dtype=torch.int32, device=dev),
+            })
+        torch.cuda.synchronize()
+
+    def step(self):
+        from mla_kv_quant_amd import kernels, synth
+
+        for d in self.layers_data:
+            kernels.write_rows(d["x"], d["pe"], d["rt"], self.loc, self.seqs, self.positions, self.reqs,
+                               d["codes"], d["params"], d["rope"], d["hp"], d["row"], d["owner"],
+                               self.P, self.W, self.max_reqs, synth.DEFAULT_THRESHOLD, synth.DEFAULT_GAIN)
+
+    def bytes_per_layer(self) -> float:
+        D, R, n = self.D, self.R, self.n
+        kept = self.SEQS * (self.P + self.W)
+        return float(n * (2 * D + 2 * R) + n * (D // 4 + 8 * (D // 128) + 2 * R + 4) + kept * (2 * D + 4))
+
+    def flops_per_layer(self) -> float:
+        return float(2 * self.n * self.D * self.D)
+
+
+# ---------------------------------------------------------------------------
+# CPU baseline (oracle on the host cores)
+# ---------------------------------------------------------------------------
+def cpu_baseline(db: DecodeBench, seqs: int = 2):
+    from oracle import attention, layout, window
+
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    c = db.caches[0]
+    D, R, P, W, L = db.D, db.R, db.P, db.W, db.L
+    pool = {
+        "codes": c["codes"].cpu().numpy(),
+        "params": c["params"].cpu().numpy(),
+        "rope": c["rope"].cpu().view(torch.int16).numpy().view(np.uint16),
+        "hp": c["hp"].cpu().view(torch.int16).numpy().view(np.uint16),
+    }
+    pt = db.kv_indices.cpu().numpy().reshape(db.B, -1)
+    q = c["q"].cpu()
+    slots = [(pt[b][:, None] * db.PAGE + np.arange(db.PAGE)).reshape(-1) for b in range(seqs)]
+    # warm-up on a short prefix, then time `seqs` full sequences
+    attention.decode(pool, q[:1, :, :D], q[:1, :, D:], slots[:1], [1024], [1], P, W, db.sm_scale, D, "fp32")
+    t0 = time.perf_counter()
+    attention.decode(pool, q[:seqs, :, :D], q[:seqs, :, D:], slots, [L] * seqs, list(range(1, seqs + 1)),
+                     P, W, db.sm_scale, D, "fp32")
+    dt = time.perf_counter() - t0
+    per_layer_us = dt / seqs * db.B * 1e6
+    return {"value": round(per_layer_us, 1), "unit": "us/layer", "cores": threads, "kind": "port",
+            "sample": f"oracle dequantize-then-attention (torch CPU, FP32) on {seqs} of the 32 sequences "
+                      f"x 16384 tokens of layer 0, scaled x{db.B // seqs} to one layer"}
+
+
+def read_traffic():
+    """HBM bytes per decode_stage1 dispatch from the committed rocprofv3 summary, if any."""
+    f = ROOT / "profiles" / "decode_cfg2_traffic.json"
+    if f.exists():
+        try:
+            return json.loads(f.read_text()).get("hbm_bytes_per_layer")
+        except Exception:
+            return None
+    return None
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py measures one GPU only (the packed-INT2 path is single-GPU here); got --gpus {args.gpus}",
+              file=sys.stderr)
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print("bench.py needs an MI355X GPU", file=sys.stderr)
+        sys.exit(2)
+    dev = "cuda:0"
+    torch.cuda.set_device(0)
+    from mla_kv_quant_amd import _lib
+
+    _lib.load()
+    t_setup = time.time()
+    db = DecodeBench(args.layers, dev)
+    print(f"[bench] decode caches written for {args.layers} layers in {time.time() - t_setup:.1f}s", file=sys.stderr,
+          flush=True)
+    candidates = [args.splits] if args.splits else [5, 8, 9, 17, 33]
+    best = None
+    for ns in candidates:
+        db.alloc_scratch(ns)
+        db.set_splits(ns)
+        ms = time_loop(db.step, 2, 1)
+        print(f"[bench] splits={ns}: {ms * 1000 / args.layers:.2f} us/layer", file=sys.stderr, flush=True)
+        if best is None or ms < best[1]:
+            best = (ns, ms)
+    db.alloc_scratch(best[0])
+    db.set_splits(best[0])
+    ms = time_loop(db.step, args.steps, args.warmup)
+    us_layer = ms * 1000.0 / args.layers
+    bpl = db.bytes_per_layer()
+    achieved = bpl / (us_layer * 1e-6) / 1e9
+    print(f"[bench] decode: {us_layer:.2f} us/layer, {achieved:.0f} GB/s", file=sys.stderr, flush=True)
+
+    result = {
+        "metric": "INT2 MLA decode attn us/layer (cfg2: B=32 x 16K, H=16, D=512, R=64)",
+        "value": round(us_layer, 3),
+        "unit": "us/layer",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": False,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "int2-cache/bf16-mfma/fp32-acc",
+        "data": "synthetic (seeded N(0,1) latents, 1% outlier channels x20, seeded orthogonal rotations)",
+        "config": {"workload": "cfg2 decode: batch 32 x context 16384, 16 heads, latent 512, rope 64, "
+                               "s4r16 window, page 64 shuffled, 27 layers with own buffers",
+                   "batch": db.B, "context": db.L, "heads": db.H, "layers": args.layers,
+                   "num_kv_splits": best[0]},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": read_traffic(),
+                     "algorithmic_bytes_per_layer": bpl,
+                     "mfma_frac": round(db.flops_per_layer() / (us_layer * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4)},
+    }
+    if not args.no_writer:
+        del db.caches
+        torch.cuda.empty_cache()
+        wb = WriterBench(args.layers, dev)
+        wms = time_loop(wb.step, max(3, args.steps // 2), args.warmup)
+        wus = wms * 1000.0 / args.layers
+        wach = wb.bytes_per_layer() / (wus * 1e-6) / 1e9
+        result["writer"] = {
+            "workload": "cfg1 writer: 64 seqs x 2048-token prefill chunk, 27 layers with own buffers",
+            "mtokens_per_s": round(wb.n * args.layers / (wms * 1e-3) / 1e6, 1),
+            "us_per_layer": round(wus, 3),
+            "hbm_achieved_gbs": round(wach, 1),
+            "hbm_frac": round(wach / HBM_PEAK_GBS, 4),
+            "mfma_frac": round(wb.flops_per_layer() / (wus * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
+        }
+        print(f"[bench] writer: {wus:.2f} us/layer, {result['writer']['mtokens_per_s']} Mtok/s", file=sys.stderr,
+              flush=True)
+        del wb
+        torch.cuda.empty_cache()
+        if not args.no_cpu:
+            db = DecodeBench(1, dev)
+    if not args.no_cpu:
+        result["cpu_baseline"] = cpu_baseline(db)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -108,8 +108,8 @@ int rolaq_prepare_gf_splits(const int32_t* splits, int32_t* quant, int32_t* merg
  * splits 0 / -1e4) go to attn_logits fp32 [B, H, max_kv_splits + 1, D] and
  * attn_lse fp32 [B, H, max_kv_splits + 1]; the merged output to out: bf16
  * [B, H, D] with strides (out_stride_b, out_stride_h), in the rotated frame.
- * Supported shapes: (D, R, H) with D = 512, R = 64, H <= 16 or D = 256, R = 32,
- * H <= 16 or 33 <= H <= 48.
+ * Supported shapes: (D, R) = (512, 64) or (256, 32), 1 <= H <= 128 (one block
+ * per 16 heads); window P + W <= 32.
  */
 int rolaq_decode_fwd(const void* q, int64_t q_stride_b, int64_t q_stride_h, const uint8_t* codes,
                      const float* params, const void* rope_buf, const void* hp_c,

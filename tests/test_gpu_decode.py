@@ -29,6 +29,8 @@ CASES = [
     ("dsv2_paged16", 512, 64, 16, [130, 511, 1000], 16, [3, 5, 9]),
     ("minicpm3_h40", 256, 32, 40, [1, 25, 64, 513, 1200], 32, [2, 3, 4, 6, 9]),
     ("minicpm3_h16", 256, 32, 16, [19, 300, 901], 1, [1, 2, 7]),
+    ("dsv2_h32_tp4", 512, 64, 32, [3, 90, 1025], 64, [2, 4, 9]),
+    ("dsv2_h8", 512, 64, 8, [48, 777], 16, [3, 6]),
 ]
 
 
