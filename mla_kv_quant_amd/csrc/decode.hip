@@ -5,13 +5,14 @@
 // deployment/patches/rolaq_sglang.patch:51-111); arithmetic of
 // mla_quant/cache.py:1007-1073 + eager MLA attention.
 //
-// Work split: grid (B, max_splits + 1). Block (b, s) with s < nq = max(ns_b - 1, 1)
-// handles a contiguous range of 32-token tiles of the INT2 positions
-// [P, L_b - W); block s == nq handles the <= P + W BF16 window rows; larger s
-// exit. A second kernel merges the nq + 1 partials by LSE.
+// Work split: grid (B * ceil(H / 16), max_splits + 1). Block (b, head group,
+// s) with s < nq = max(ns_b - 1, 1) handles a contiguous range of 32-token
+// tiles of the INT2 positions [P, L_b - W) for 16 heads; block s == nq handles
+// the <= P + W BF16 window rows; larger s exit. A second kernel merges the
+// nq + 1 partials by LSE.
 //
-// INT2 split, per wave (4 waves per block, tiles interleaved across waves):
-//   scores  S^T[t, h] = sum_g scale_tg (sum_j q'_hj v_tj - 4 Q'_hg) - scale_tg zero_tg Qsum_hg
+// INT2 split arithmetic (per 32-token tile):
+//   scores  S^T[t, h] = sum_g scale_tg (sum_j q'_hj v_tj - 4 Q'_hg - zero_tg Qsum_hg)
 //           on bf16 MFMA 16x16x32 with M = 16 tokens, N = 16 heads, K = latent.
 //           v_tj = 4 + c_tj 2^(e-5) is the code masked into a bf16 mantissa and
 //           q'_hj = q_hj 2^(5-e) the matching exact rescale of the query.
@@ -22,13 +23,10 @@
 //           p'_g enters as a bf16 hi + lo pair (two MFMAs), so the output is
 //           FP32-accurate. A ones-column MFMA accumulates SP_g = sum_t p'_g exactly
 //           as the output MFMA sees it, so o = (O - 4 SP_g) 2^(5-e) - sum_t p'_g zero_tg.
-#include <type_traits>
-
 #include "rolaq_common.h"
 #include "rolaq_args.h"
 
 namespace rolaq {
-
 
 struct SeqCtx {
   const int32_t* idx;
@@ -36,6 +34,7 @@ struct SeqCtx {
   int shift;
 };
 
+// Cache slot of position pos (clamped into [0, L)): page table entry * page + offset.
 __device__ __forceinline__ int64_t slot_of(const SeqCtx& c, int pos) {
   pos = min(max(pos, 0), c.L - 1);
   const int64_t page = c.idx[pos >> c.shift];
@@ -47,44 +46,30 @@ __device__ __forceinline__ int ring_row(int64_t req, int pos, int P, int W) {
   return int(1 + req * (P + W) + inner);
 }
 
-template <int N>
-__device__ __forceinline__ void load_words(const uint8_t* p, uint32_t (&w)[N]) {
-  static_assert(N % 2 == 0, "");
-  if constexpr (N % 4 == 0) {
-#pragma unroll
-    for (int i = 0; i < N; i += 4) {
-      const u32x4 v = *reinterpret_cast<const u32x4*>(p + 4 * i);
-      w[i] = v.x; w[i + 1] = v.y; w[i + 2] = v.z; w[i + 3] = v.w;
-    }
-  } else {
-#pragma unroll
-    for (int i = 0; i < N; i += 2) {
-      const u32x2 v = *reinterpret_cast<const u32x2*>(p + 4 * i);
-      w[i] = v.x; w[i + 1] = v.y;
-    }
-  }
-}
+__device__ __forceinline__ u32x4 lds128(const uint8_t* p) { return *reinterpret_cast<const u32x4*>(p); }
+__device__ __forceinline__ f32x4 lds128f(const uint8_t* p) { return *reinterpret_cast<const f32x4*>(p); }
 
 // ---------------------------------------------------------------------------
 // Window split: attention over the BF16 sink/recent rows of one sequence.
 // The <= MAXW rows (hp_c ring rows + rope) are staged into LDS with 16-byte
-// loads, then thread t = (head h = t & 15 (+16 hb), chunk c = t >> 4) forms
+// loads, then thread t < 256 = (head h = t & 15, chunk c = t >> 4) forms
 // partial dots over D/16 latent + R/16 rope dims; waves reduce through LDS.
 // Writes the normalised partial and natural-log LSE at split slot.
+// Every thread of the block reaches every barrier.
 // ---------------------------------------------------------------------------
 constexpr int kMaxWindow = 32;
-
 template <int D, int R>
 constexpr int window_rows_bytes() { return kMaxWindow * (D + R) * 2; }
 constexpr int window_part_floats() { return (4 * 16 + 16) * kMaxWindow + 16; }
 
-template <int D, int R, int NHB>
+template <int D, int R>
 __device__ void window_split(const DecodeArgs& a, int b, int h0, int slot_split, const SeqCtx& sc,
                              int64_t req, float* smem, uint8_t* rows_mem) {
   constexpr int MAXW = kMaxWindow;
   constexpr int FC = D / 16, RC = R / 16;
   constexpr int ROWE = D + R;  // staged row: latent | rope (bf16 elements)
   const int t = threadIdx.x, h16 = t & 15, c = t >> 4, lane = t & 63, wave = t >> 6;
+  const bool act = t < 256;
   const int L = sc.L, P = a.P, W = a.W;
   // window positions in increasing order: [0, min(P, L)) U [max(L - W, P), L)
   const int n_sink = min(P, L);
@@ -95,7 +80,7 @@ __device__ void window_split(const DecodeArgs& a, int b, int h0, int slot_split,
   float* prob = sc_part + 4 * 16 * MAXW;                              // [16][MAXW] + 16
   // stage rows: D/8 + R/8 16-byte chunks per row
   constexpr int CPR = (D + R) / 8;
-  for (int k = t; k < nw * CPR; k += 256) {
+  for (int k = t; k < nw * CPR; k += blockDim.x) {
     const int i = k / CPR, ch = k % CPR;
     const int pos = i < n_sink ? i : rec_lo + (i - n_sink);
     const uint16_t* src = ch < D / 8 ? a.hp + (int64_t)ring_row(req, pos, P, W) * D + 8 * ch
@@ -103,9 +88,9 @@ __device__ void window_split(const DecodeArgs& a, int b, int h0, int slot_split,
     *reinterpret_cast<u32x4*>(rows + i * ROWE + 8 * ch) = *reinterpret_cast<const u32x4*>(src);
   }
   __syncthreads();
-  for (int hb = 0; hb < NHB; ++hb) {
-    const int h = h0 + 16 * hb + h16;
-    const bool hv = h < a.H;
+  const int h = h0 + h16;
+  const bool hv = h < a.H;
+  if (act) {
     const uint16_t* qh = a.q + b * a.q_sb + (int64_t)min(h, a.H - 1) * a.q_sh;
     float qv[FC], qr[RC];
 #pragma unroll
@@ -132,26 +117,28 @@ __device__ void window_split(const DecodeArgs& a, int b, int h0, int slot_split,
       acc = wave_sum_over_groups(acc);  // chunks c, c^1, c^2, c^3 of this wave
       if (lane < 16) sc_part[(wave * 16 + h16) * MAXW + i] = acc;
     }
-    __syncthreads();
-    if (c == 0) {
-      float m = -3.0e38f, l = 0.f;
-      for (int i = 0; i < nw; ++i) {
-        const float s = (sc_part[h16 * MAXW + i] + sc_part[(16 + h16) * MAXW + i] +
-                         sc_part[(32 + h16) * MAXW + i] + sc_part[(48 + h16) * MAXW + i]) *
-                        a.sm_scale * kLog2e;
-        prob[h16 * MAXW + i] = s;
-        m = fmaxf(m, s);
-      }
-      for (int i = 0; i < nw; ++i) {
-        const float p = __builtin_amdgcn_exp2f(prob[h16 * MAXW + i] - m);
-        prob[h16 * MAXW + i] = p;
-        l += p;
-      }
-      const int64_t li = ((int64_t)b * a.H + h) * a.S1 + slot_split;
-      if (hv) a.lse[li] = nw ? (m + __log2f(l)) * kLn2 : kNeutralLse;
-      prob[16 * MAXW + h16] = nw ? 1.f / l : 0.f;
+  }
+  __syncthreads();
+  if (t < 16) {
+    float m = -3.0e38f, l = 0.f;
+    for (int i = 0; i < nw; ++i) {
+      const float s = (sc_part[h16 * MAXW + i] + sc_part[(16 + h16) * MAXW + i] +
+                       sc_part[(32 + h16) * MAXW + i] + sc_part[(48 + h16) * MAXW + i]) *
+                      a.sm_scale * kLog2e;
+      prob[h16 * MAXW + i] = s;
+      m = fmaxf(m, s);
     }
-    __syncthreads();
+    for (int i = 0; i < nw; ++i) {
+      const float p = __builtin_amdgcn_exp2f(prob[h16 * MAXW + i] - m);
+      prob[h16 * MAXW + i] = p;
+      l += p;
+    }
+    const int64_t li = ((int64_t)b * a.H + h) * a.S1 + slot_split;
+    if (hv) a.lse[li] = nw ? (m + __log2f(l)) * kLn2 : kNeutralLse;
+    prob[16 * MAXW + h16] = nw ? 1.f / l : 0.f;
+  }
+  __syncthreads();
+  if (act) {
     const float inv = prob[16 * MAXW + h16];
     float o[FC];
 #pragma unroll
@@ -167,50 +154,30 @@ __device__ void window_split(const DecodeArgs& a, int b, int h0, int slot_split,
 #pragma unroll
       for (int k = 0; k < FC; k += 4) *reinterpret_cast<f32x4*>(dst + k) = f32x4{o[k] * inv, o[k + 1] * inv, o[k + 2] * inv, o[k + 3] * inv};
     }
-    __syncthreads();
   }
 }
 
 // ---------------------------------------------------------------------------
-// Stage 1: one block per (split, sequence).
-//
-// Each wave walks its 32-token tiles with a one-tile software pipeline: the
-// raw 16-byte chunks of tile i+1 (codes, rope, params) are loaded into
-// registers while tile i is computed from the wave's LDS buffer, then written
-// to that buffer. With PAGED (page size a multiple of 32) a tile occupies 32
-// consecutive slots, so every lane's load offset is a per-lane constant plus
-// one uniform page base.
+// LDS image of one 32-token tile: codes (32 x D/4 B), rope (32 x 2R B), params
+// (32 x 8 NG B). Code and rope rows are stored as 16-byte chunks with chunk c
+// of token t at slot t*CH + (c ^ (t % CH)): sixteen lanes reading one chunk
+// column of sixteen tokens then spread over the LDS banks.
 // ---------------------------------------------------------------------------
 template <int D, int R>
 struct Geo {
   static constexpr int NG = D / 128;      // quantization groups
   static constexpr int KR = R / 32;       // rope K-blocks
-  static constexpr int NB = D / 16;       // output N-blocks (16 features each)
-  static constexpr int SW = 4 * NG;       // bytes of one superword (word s of every group)
   static constexpr int ROWB = D / 4;      // packed bytes per token
   static constexpr int PB = 8 * NG;       // param bytes per token
   static constexpr int RBYTES = 2 * R;    // rope bytes per token
   static constexpr int CCH = ROWB / 16;   // 16-byte chunks per row (8 / 4)
   static constexpr int RCH = RBYTES / 16;
-  static constexpr int PCH = PB / 16;
-  static constexpr int CL = 32 * CCH / 64;  // DMA loads (1 KB each) per tile
-  static constexpr int RL = 32 * RCH / 64;
-  static constexpr int PL = (32 * PCH + 63) / 64;
   static constexpr int OFF_R = 32 * ROWB;
   static constexpr int OFF_P = OFF_R + 32 * RBYTES;
-  static constexpr int TILE_LDS = OFF_P + 64 * 16 * PL;
-  // chunk c of token t sits at 16-byte slot t*CCH + (c ^ (t % CCH)): rows read
-  // by 16 lanes at once then spread over the LDS banks
+  static constexpr int TILE_LDS = OFF_P + 32 * PB;
   __device__ static constexpr int cslot(int t, int c) { return t * CCH + (c ^ (t & (CCH - 1))); }
   __device__ static constexpr int rslot(int t, int c) { return t * RCH + (c ^ (t & (RCH - 1))); }
 };
-
-// One 16-byte direct global->LDS load per lane (global_load_lds_dwordx4). The
-// LDS destination is wave-uniform: lane i lands at dst + 16 i.
-__device__ __forceinline__ void lds_dma16(const uint8_t* src, uint8_t* dst) {
-  typedef __attribute__((address_space(3))) void lds_t;
-  __builtin_amdgcn_global_load_lds(src, (lds_t*)dst, 16, 0, 0);
-}
 
 __device__ __forceinline__ uint32_t and_or(uint32_t x, uint32_t m, uint32_t b) {
   uint32_t d;
@@ -232,286 +199,77 @@ __device__ __forceinline__ void unpack_word_fast(uint32_t w, uint32_t d[8], uint
   d[7] = and_or(w12, 0x000C000Cu, base);
 }
 
-// State of one wave's INT2 split (everything the tile loop updates or reads).
-template <int D, int R, int NHB>
-struct WaveState {
-  static constexpr int NG = D / 128, KR = R / 32, NB = D / 16;
-  f32x4 O[NHB][NB];
-  f32x4 SP[NHB][NG];
-  float m_run[NHB], l_run[NHB], zp[NHB][NG];
-  float q4[NHB][NG], qsum[NHB][NG];
-  u32x4 qr[NHB][KR];
-  const u32x4 (*s_qs)[4 * NG][64];
-  u32x4 ones;
-  uint32_t perm_sel, vbase;
-  int lane, gq, la, lo, hi;
-  float scale_log2;
-};
-
-// One 32-token tile from the wave's LDS buffer tl; FULL tiles lie inside [lo, hi).
-template <int D, int R, int NHB, bool full>
-__device__ __forceinline__ void tile_compute(WaveState<D, R, NHB>& st, int tile, const uint8_t* tl) {
-  using G = Geo<D, R>;
-  constexpr int NG = G::NG, KR = G::KR, NB = G::NB, SW = G::SW, PB = G::PB;
-  constexpr int TILE = 32;
-  auto& O = st.O;
-  auto& SP = st.SP;
-  auto& m_run = st.m_run;
-  auto& l_run = st.l_run;
-  auto& zp = st.zp;
-  const auto& q4 = st.q4;
-  const auto& qsum = st.qsum;
-  const auto& qr = st.qr;
-  const auto s_qs = st.s_qs;
-  const u32x4 ones = st.ones;
-  const uint32_t perm_sel = st.perm_sel, vbase = st.vbase;
-  const int lane = st.lane, gq = st.gq, la = st.la, lo = st.lo, hi = st.hi;
-  const float scale_log2 = st.scale_log2;
-    const int p0 = tile * TILE;
-    // -- scores: S^T[token, head] -----------------------------------------------
-    float s[2][NHB][4];
-    uint32_t cw[2][2 * NG];  // codes of token 16mb + la, superwords 2gq, 2gq+1
-#pragma unroll
-    for (int mb = 0; mb < 2; ++mb) {
-      const int t = 16 * mb + la;
-      if constexpr (NG == 4) {
-        const u32x4 v0 = *reinterpret_cast<const u32x4*>(tl + 16 * G::cslot(t, 2 * gq));
-        const u32x4 v1 = *reinterpret_cast<const u32x4*>(tl + 16 * G::cslot(t, 2 * gq + 1));
-        cw[mb][0] = v0.x; cw[mb][1] = v0.y; cw[mb][2] = v0.z; cw[mb][3] = v0.w;
-        cw[mb][4] = v1.x; cw[mb][5] = v1.y; cw[mb][6] = v1.z; cw[mb][7] = v1.w;
-      } else {
-        const u32x4 v0 = *reinterpret_cast<const u32x4*>(tl + 16 * G::cslot(t, gq));
-        cw[mb][0] = v0.x; cw[mb][1] = v0.y; cw[mb][2] = v0.z; cw[mb][3] = v0.w;
-      }
-#pragma unroll
-      for (int hb = 0; hb < NHB; ++hb) {
-        f32x4 acc = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int kr = 0; kr < KR; ++kr) {
-          const u32x4 ro = *reinterpret_cast<const u32x4*>(tl + G::OFF_R + 16 * G::rslot(t, 4 * kr + gq));
-          acc = mfma16x16x32(ro, qr[hb][kr], acc);
-        }
-#pragma unroll
-        for (int j = 0; j < 4; ++j) s[mb][hb][j] = acc[j];
-      }
-    }
-    // (scale, zero) of groups 2gp, 2gp+1 for this lane's C-layout token 16mb + 4gq + j
-    auto param2 = [&](int mb, int j, int gp) -> f32x4 {
-      f32x4 v = *reinterpret_cast<const f32x4*>(tl + G::OFF_P + (16 * mb + 4 * gq + j) * PB + 16 * gp);
-      if constexpr (!full) {
-        // masked positions may hold rows that were never written: use 0
-        const int pos = p0 + 16 * mb + 4 * gq + j;
-        if (pos < lo || pos >= hi) v = f32x4{0.f, 0.f, 0.f, 0.f};
-      }
-      return v;
-    };
-#pragma unroll
-    for (int g = 0; g < NG; ++g) {
-      // a compiler-level fence per group: the loads below are not merged with
-      // (or hoisted above) those of other groups, which bounds register use
-      asm volatile("" ::: "memory");
-      f32x4 pv[2][4];
-#pragma unroll
-      for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) pv[mb][j] = param2(mb, j, g / 2);
-      float scl[2][4], szr[2][4];
-#pragma unroll
-      for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const float sv = (g & 1) ? pv[mb][j].z : pv[mb][j].x;
-          const float zv = (g & 1) ? pv[mb][j].w : pv[mb][j].y;
-          scl[mb][j] = sv;
-          szr[mb][j] = sv * zv;
-        }
-      u32x4 kop[2][4];
-#pragma unroll
-      for (int mb = 0; mb < 2; ++mb) {
-        uint32_t d0[8], d1[8];
-        unpack_word_fast(cw[mb][g], d0, vbase);        // superword 2gq
-        unpack_word_fast(cw[mb][NG + g], d1, vbase);   // superword 2gq + 1
-        kop[mb][0] = u32x4{d0[0], d0[1], d0[2], d0[3]};
-        kop[mb][1] = u32x4{d0[4], d0[5], d0[6], d0[7]};
-        kop[mb][2] = u32x4{d1[0], d1[1], d1[2], d1[3]};
-        kop[mb][3] = u32x4{d1[4], d1[5], d1[6], d1[7]};
-      }
-#pragma unroll
-      for (int hb = 0; hb < NHB; ++hb) {
-        const float init = -q4[hb][g];
-        f32x4 acc[2] = {{init, init, init, init}, {init, init, init, init}};
-#pragma unroll
-        for (int kbl = 0; kbl < 4; ++kbl) {
-          const u32x4 qv = s_qs[hb][4 * g + kbl][lane];
-          acc[0] = mfma16x16x32(kop[0][kbl], qv, acc[0]);
-          acc[1] = mfma16x16x32(kop[1][kbl], qv, acc[1]);
-        }
-#pragma unroll
-        for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-          for (int j = 0; j < 4; ++j)
-            s[mb][hb][j] = fmaf(scl[mb][j], acc[mb][j], fmaf(-szr[mb][j], qsum[hb][g], s[mb][hb][j]));
-      }
-      __builtin_amdgcn_sched_barrier(0);  // keep each group's LDS reads within the group
-    }
-
-    // -- online softmax (log2 domain, lazy rescale) ------------------------------
-    float p[2][NHB][4];
-#pragma unroll
-    for (int hb = 0; hb < NHB; ++hb) {
-      float mt = -1.0e30f;
-#pragma unroll
-      for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          float v = s[mb][hb][j] * scale_log2;
-          if constexpr (!full) {
-            const int pos = p0 + 16 * mb + 4 * gq + j;
-            if (pos < lo || pos >= hi) v = -1.0e30f;
-          }
-          s[mb][hb][j] = v;
-          mt = fmaxf(mt, v);
-        }
-      mt = wave_max_over_groups(mt);
-      // keep exp2 arguments <= 8: rescale only when a head's max grows past that
-      if (__any(mt > m_run[hb] + 8.0f)) {
-        const float m_new = fmaxf(m_run[hb], mt);
-        const float alpha = __builtin_amdgcn_exp2f(m_run[hb] - m_new);
-        l_run[hb] *= alpha;
-#pragma unroll
-        for (int g = 0; g < NG; ++g) zp[hb][g] *= alpha;
-        float ao[4];
-#pragma unroll
-        for (int j = 0; j < 4; ++j) ao[j] = __shfl(alpha, 4 * gq + j);
-        // rare: one accumulator tile at a time keeps the register footprint small
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb) {
-#pragma unroll
-          for (int j = 0; j < 4; ++j) O[hb][nb][j] *= ao[j];
-          __builtin_amdgcn_sched_barrier(0);
-        }
-#pragma unroll
-        for (int g = 0; g < NG; ++g) {
-#pragma unroll
-          for (int j = 0; j < 4; ++j) SP[hb][g][j] *= ao[j];
-          __builtin_amdgcn_sched_barrier(0);
-        }
-        m_run[hb] = m_new;
-      }
-      float ls = 0.f;
-#pragma unroll
-      for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const float e = __builtin_amdgcn_exp2f(s[mb][hb][j] - m_run[hb]);
-          p[mb][hb][j] = e;
-          ls += e;
-        }
-      l_run[hb] += ls;
-    }
-    __builtin_amdgcn_sched_barrier(0);
-
-    // -- output: O += P'_g V_g per group -------------------------------------------
-    uint32_t co[8][NG];  // tokens tau(i): word of every group in superword la/2
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      const int t = (i < 4 ? 4 * gq + i : 16 + 4 * gq + (i - 4));
-      if constexpr (NG == 4) {
-        const u32x4 v = *reinterpret_cast<const u32x4*>(tl + 16 * G::cslot(t, la >> 1));
-        co[i][0] = v.x; co[i][1] = v.y; co[i][2] = v.z; co[i][3] = v.w;
-      } else {
-        const u32x2 v = *reinterpret_cast<const u32x2*>(tl + 16 * G::cslot(t, la >> 2) + 8 * ((la >> 1) & 1));
-        co[i][0] = v.x; co[i][1] = v.y;
-      }
-    }
-#pragma unroll
-    for (int g = 0; g < NG; ++g) {
-      asm volatile("" ::: "memory");
-      f32x4 pv[2][4];
-#pragma unroll
-      for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) pv[mb][j] = param2(mb, j, g / 2);
-      float scl[2][4], zr[2][4];
-#pragma unroll
-      for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          scl[mb][j] = (g & 1) ? pv[mb][j].z : pv[mb][j].x;
-          zr[mb][j] = (g & 1) ? pv[mb][j].w : pv[mb][j].y;
-        }
-      // p'_g = p * scale as a bf16 hi + lo pair: the two output MFMAs see
-      // hi + lo = p'_g to ~2^-17, so the contraction is FP32-accurate.
-      u32x4 Ph[NHB], Pl[NHB];
-#pragma unroll
-      for (int hb = 0; hb < NHB; ++hb) {
-        float pg[8];
-#pragma unroll
-        for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-          for (int j = 0; j < 4; ++j) pg[4 * mb + j] = p[mb][hb][j] * scl[mb][j];
-        uint32_t hv[4], lv[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          hv[r] = pack_bf16(pg[2 * r], pg[2 * r + 1]);
-          lv[r] = pack_bf16(pg[2 * r] - bf16_lo(hv[r]), pg[2 * r + 1] - bf16_hi(hv[r]));
-        }
-        Ph[hb] = u32x4{hv[0], hv[1], hv[2], hv[3]};
-        Pl[hb] = u32x4{lv[0], lv[1], lv[2], lv[3]};
-        float z = zp[hb][g];
-#pragma unroll
-        for (int mb = 0; mb < 2; ++mb)
-#pragma unroll
-          for (int j = 0; j < 4; ++j) z = fmaf(pg[4 * mb + j], zr[mb][j], z);
-        zp[hb][g] = z;
-      }
-      uint32_t dr[4][8];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const uint32_t x = __builtin_amdgcn_perm(co[2 * r + 1][g], co[2 * r][g], perm_sel);
-        unpack_word_fast(x, dr[r], vbase);
-      }
-#pragma unroll
-      for (int nbl = 0; nbl < 8; ++nbl) {
-        const u32x4 bv = {dr[0][nbl], dr[1][nbl], dr[2][nbl], dr[3][nbl]};
-#pragma unroll
-        for (int hb = 0; hb < NHB; ++hb) {
-          O[hb][8 * g + nbl] = mfma16x16x32(Ph[hb], bv, O[hb][8 * g + nbl]);
-          O[hb][8 * g + nbl] = mfma16x16x32(Pl[hb], bv, O[hb][8 * g + nbl]);
-        }
-      }
-#pragma unroll
-      for (int hb = 0; hb < NHB; ++hb) {
-        SP[hb][g] = mfma16x16x32(Ph[hb], ones, SP[hb][g]);
-        SP[hb][g] = mfma16x16x32(Pl[hb], ones, SP[hb][g]);
-      }
-      __builtin_amdgcn_sched_barrier(0);
-    }
+// One 16-byte direct global->LDS load per lane (global_load_lds_dwordx4). The
+// LDS destination is wave-uniform: lane i lands at dst + 16 i.
+__device__ __forceinline__ void lds_dma16(const uint8_t* src, uint8_t* dst) {
+  typedef __attribute__((address_space(3))) void lds_t;
+  __builtin_amdgcn_global_load_lds(src, (lds_t*)dst, 16, 0, 0);
 }
 
-template <int D, int R, int NHB, bool PAGED>
-__global__ __launch_bounds__(256, 1) void decode_stage1(DecodeArgs a) {
-  using G = Geo<D, R>;
-  constexpr int NG = G::NG, KR = G::KR, NB = G::NB, SW = G::SW, ROWB = G::ROWB, PB = G::PB;
-  constexpr int TILE = 32;
-  static_assert(R % 32 == 0 && D % 256 == 0, "unsupported shape");
+// Page-table entries a wave needs for its share of one tile's direct loads:
+// with pages of >= 32 tokens the tile's one page, else one entry per load
+// instruction and lane. They are loaded a step before use, so the wait for
+// them never waits for the tile loads issued in between.
+template <int CLW, int RLW, bool PAGED>
+struct TilePages {
+  int pg;  // PAGED
+  int cs[PAGED ? 1 : CLW], rs[PAGED ? 1 : RLW], ps;
+};
 
-  // Three tile-ring buffers as separate LDS objects (so the compiler's wait
-  // insertion can tell a read of one from the DMA in flight to another); after
-  // the loop the first holds the merge buffer, and the window split uses the
-  // first two for its partial sums and staged rows.
-  constexpr int RING = 4 * G::TILE_LDS;  // 4 waves
+constexpr int kPairs = 4;                // wave pairs per block
+constexpr int kThreads = 128 * kPairs;   // 8 waves
+constexpr float kNoRef = -1.0e30f;       // "no score yet" / masked score (log2 units)
+constexpr float kRefSlack = 64.f;        // max exp2 argument before a split is redone
+
+// ---------------------------------------------------------------------------
+// Stage 1 INT2 splits. The block's 8 waves form 4 pairs; pair pr takes tiles
+// my_begin + pr + 4k. For each tile, wave wh of a pair
+//   phase 1: computes the scores of tokens 16wh..16wh+15 over the whole latent
+//            and rope and leaves them in LDS for its partner;
+//   phase 2: after the block barrier, takes the softmax of all 32 tokens (the
+//            same values in both waves) and accumulates the output of its own
+//            half of the quantization groups.
+// Each wave keeps only its half of the output accumulators, so a wave fits in
+// 256 registers and two waves share a SIMD.
+//
+// Tiles reach LDS by direct global->LDS loads, three buffers per pair; both
+// waves of a pair load half a tile each. The barrier of step k follows a
+// vmcnt(0) wait, so after it tile k+1 is complete for both waves, and every
+// wave is done with the buffer of tile k-1, which then receives tile k+2.
+//
+// The softmax uses a fixed reference per head: the max of the pair's first
+// tile. Later scores may exceed it by up to kRefSlack (exp2 <= 2^64 stays
+// finite in every accumulator); a split where any score goes further is
+// recomputed with the true max, so the tile loop carries no rescaling.
+// ---------------------------------------------------------------------------
+template <int D, int R, bool PAGED>
+__global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
+  using G = Geo<D, R>;
+  constexpr int NG = G::NG, KR = G::KR, ROWB = G::ROWB, PB = G::PB, CCH = G::CCH, RCH = G::RCH;
+  constexpr int GW = NG / 2;                  // output groups per wave
+  constexpr int CLW = CCH / 4, RLW = RCH / 4; // direct loads per wave and tile (codes, rope)
+  constexpr int PCT = PB / 16;                // 16-byte param chunks per token
+  constexpr int TILE = 32;
+  constexpr int RING = kPairs * G::TILE_LDS;
+  static_assert(R % 32 == 0 && D % 256 == 0, "unsupported shape");
   static_assert(16 * D * 4 <= RING, "merge buffer does not fit in one ring buffer");
+  static_assert(window_rows_bytes<D, R>() <= RING && window_part_floats() * 4 <= RING, "window scratch");
+  using Pages = TilePages<CLW, RLW, PAGED>;
+
+  // Three tile buffers as separate LDS objects, so the compiler's wait
+  // insertion can tell reads of one from direct loads in flight to another.
   __shared__ __attribute__((aligned(16))) uint8_t s_r0[RING];
   __shared__ __attribute__((aligned(16))) uint8_t s_r1[RING];
   __shared__ __attribute__((aligned(16))) uint8_t s_r2[RING];
-  __shared__ float s_ml[4][NHB * 16][2];
-  // score-MFMA B operands of the query (one copy per block): [hb][K-block][lane]
-  __shared__ __attribute__((aligned(16))) u32x4 s_qs[NHB][4 * NG][64];
-  // blockIdx.x = (sequence, head group of 16 NHB heads); split-major grid: the
-  // real splits of every sequence dispatch before the surplus (empty) ones
-  const int nhg = (a.H + 16 * NHB - 1) / (16 * NHB);
-  const int b = blockIdx.x / nhg, h0 = 16 * NHB * (blockIdx.x % nhg), split = blockIdx.y;
+  __shared__ f32x4 s_x[kPairs][2][2][64];  // phase-1 scores [pair][step parity][wave of pair][lane]
+  // score-MFMA B operands of the query: [group][K-block][lane]
+  __shared__ __attribute__((aligned(16))) u32x4 s_qs[NG][4][64];
+  __shared__ __attribute__((aligned(16))) u32x4 s_qr[KR][64];  // rope B operands
+  __shared__ f32x2 s_qq[NG][16];           // per group and head: Qsum, 4 Q'
+  __shared__ float s_ml[kPairs][16][2];    // per pair and head: reference max, sum
+
+  const int nhg = (a.H + 15) / 16;
+  const int b = blockIdx.x / nhg, h0 = 16 * (blockIdx.x % nhg), split = blockIdx.y;
   const int ns = a.num_kv_splits[b];
   const int nq = min(max(ns - 1, 1), a.S1 - 1);
   if (split > nq) return;
@@ -524,11 +282,15 @@ __global__ __launch_bounds__(256, 1) void decode_stage1(DecodeArgs a) {
   const int64_t req = a.req_idx[b];
 
   if (split == nq) {
-    window_split<D, R, NHB>(a, b, h0, split, sc, req, reinterpret_cast<float*>(s_r0), s_r1);
+    window_split<D, R>(a, b, h0, split, sc, req, reinterpret_cast<float*>(s_r0), s_r1);
     return;
   }
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  // the wave index is uniform: tile indices, LDS bases and page lookups then
+  // live in scalar registers
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int pr = wave >> 1, wh = wave & 1;
   const int gq = lane >> 4, la = lane & 15;
   const int L = sc.L;
   const int lo = min(a.P, L), hi = max(L - a.W, lo);
@@ -537,23 +299,21 @@ __global__ __launch_bounds__(256, 1) void decode_stage1(DecodeArgs a) {
   const int per = (ntiles + nq - 1) / nq;
   const int my_begin = t_first + min(split * per, ntiles);
   const int my_end = t_first + min((split + 1) * per, ntiles);
+  // pair pr computes tiles tile0 + kPairs * k, k < nmine; the block runs kmax steps
+  const int kmax = (my_end - my_begin + kPairs - 1) / kPairs;
+  const int tile0 = my_begin + pr;
+  const int nmine = tile0 < my_end ? (my_end - tile0 + kPairs - 1) / kPairs : 0;
 
-  // ---- query operands -----------------------------------------------------------
-  // s_qs[hb][4g+kbl]: B operand of the score MFMA, lane (gq, la) = head la+16hb,
-  // element pair r of K-block kbl <-> in-group features 16s+k and 16s+k+8 with
-  // s = 2gq + kbl/2, k = 4(kbl%2) + r, scaled by 2^(5-e_k). Wave hb%4 stores
-  // head block hb; every wave keeps the per-head sums it needs.
-  WaveState<D, R, NHB> st;
-  auto& qr = st.qr;
-  auto& q4 = st.q4;
-  auto& qsum = st.qsum;
-#pragma unroll
-  for (int hb = 0; hb < NHB; ++hb) {
-    const int h = h0 + 16 * hb + la;
+  // ---- query operands (wave g < NG prepares group g) ---------------------------
+  // s_qs[g][kbl]: lane (gq, la) = head la, element pair r of K-block kbl <->
+  // in-group features 16s+k and 16s+k+8 with s = 2gq + kbl/2, k = 4(kbl%2) + r,
+  // scaled by 2^(5-e_k).
+  {
+    const int h = h0 + la;
     const bool hv = h < a.H;
     const uint16_t* qh = a.q + b * a.q_sb + (int64_t)min(h, a.H - 1) * a.q_sh;
-#pragma unroll
-    for (int g = 0; g < NG; ++g) {
+    if (wave < NG) {
+      const int g = wave;
       float s_sum = 0.f, s_w = 0.f;
 #pragma unroll
       for (int kbl = 0; kbl < 4; ++kbl) {
@@ -564,224 +324,340 @@ __global__ __launch_bounds__(256, 1) void decode_stage1(DecodeArgs a) {
         uint32_t outv[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const uint32_t wl = (r < 2 ? lo4.x : lo4.y), wh = (r < 2 ? hi4.x : hi4.y);
+          const uint32_t wl = (r < 2 ? lo4.x : lo4.y), whi = (r < 2 ? hi4.x : hi4.y);
           const float vl = hv ? ((r & 1) ? bf16_hi(wl) : bf16_lo(wl)) : 0.f;
-          const float vh = hv ? ((r & 1) ? bf16_hi(wh) : bf16_lo(wh)) : 0.f;
+          const float vh = hv ? ((r & 1) ? bf16_hi(whi) : bf16_lo(whi)) : 0.f;
           const float wk = pair_weight(4 * (kbl % 2) + r);
           s_sum += vl + vh;
           s_w += (vl + vh) * wk;
           outv[r] = pack_bf16(vl * wk, vh * wk);
         }
-        if (wave == (hb & 3)) s_qs[hb][4 * g + kbl][lane] = u32x4{outv[0], outv[1], outv[2], outv[3]};
+        s_qs[g][kbl][lane] = u32x4{outv[0], outv[1], outv[2], outv[3]};
       }
-      qsum[hb][g] = wave_sum_over_groups(s_sum);
-      q4[hb][g] = 4.f * wave_sum_over_groups(s_w);
-    }
-#pragma unroll
-    for (int kr = 0; kr < KR; ++kr) {
+      s_sum = wave_sum_over_groups(s_sum);
+      s_w = wave_sum_over_groups(s_w);
+      if (gq == 0) s_qq[g][la] = f32x2{s_sum, 4.f * s_w};
+    } else if (wave < NG + KR) {
+      // rope B operand of K-block kr: head la, dims 32kr + 8gq + i
+      const int kr = wave - NG;
       const u32x4 v = *reinterpret_cast<const u32x4*>(qh + D + 32 * kr + 8 * gq);
-      qr[hb][kr] = hv ? v : u32x4{0, 0, 0, 0};
+      s_qr[kr][lane] = hv ? v : u32x4{0, 0, 0, 0};
     }
   }
   __syncthreads();
   const uint32_t one = la == 0 ? 0x3F803F80u : 0u;
-  st.ones = u32x4{one, one, one, one};
-  st.perm_sel = (la & 1) ? 0x07060302u : 0x05040100u;
-  st.vbase = 0x40804080u;
-  st.s_qs = s_qs;
-  st.lane = lane;
-  st.gq = gq;
-  st.la = la;
-  st.lo = lo;
-  st.hi = hi;
-  st.scale_log2 = a.sm_scale * kLog2e;
+  const u32x4 ones = {one, one, one, one};
+  const uint32_t perm_sel = (la & 1) ? 0x07060302u : 0x05040100u;
+  const uint32_t vbase = 0x40804080u;
+  const float scale_log2 = a.sm_scale * kLog2e;
 
-  auto& O = st.O;
-  auto& SP = st.SP;
-  auto& m_run = st.m_run;
-  auto& l_run = st.l_run;
-  auto& zp = st.zp;
+  // ---- this wave's share of a tile's direct loads ------------------------------
+  // load k of kind X moves chunk q = 64 (XLW wh + k) + lane to LDS slot q.
+  int c_tok[CLW], c_off[CLW], r_tok[RLW], r_off[RLW];
 #pragma unroll
-  for (int hb = 0; hb < NHB; ++hb) {
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) O[hb][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int g = 0; g < NG; ++g) { SP[hb][g] = f32x4{0.f, 0.f, 0.f, 0.f}; zp[hb][g] = 0.f; }
-    m_run[hb] = -1.0e30f;
-    l_run[hb] = 0.f;
-  }
-
-  // ---- tile pipeline ----------------------------------------------------------
-  // Three LDS tile buffers per wave, filled by direct global->LDS loads two
-  // tiles ahead; the slot lookup for a tile runs one further tile ahead.
-  constexpr int NBUF = 3;
-  static_assert(window_rows_bytes<D, R>() <= RING && window_part_floats() * 4 <= RING, "window scratch");
-  uint8_t* const tb0 = s_r0 + wave * G::TILE_LDS;
-  uint8_t* const tb1 = s_r1 + wave * G::TILE_LDS;
-  uint8_t* const tb2 = s_r2 + wave * G::TILE_LDS;
-  // what this lane moves for every tile: 16-byte slot q of a 1 KB DMA block.
-  // PAGED: byte offsets from the tile's first slot; else token index + chunk.
-  int c_tok[G::CL], c_off[G::CL], r_tok[G::RL], r_off[G::RL];
-#pragma unroll
-  for (int k = 0; k < G::CL; ++k) {
-    const int q = 64 * k + lane, t = q / G::CCH, sl = q % G::CCH;
+  for (int k = 0; k < CLW; ++k) {
+    const int q = 64 * (CLW * wh + k) + lane, t = q / CCH, sl = q % CCH;
     c_tok[k] = t;
-    c_off[k] = 16 * (sl ^ (t & (G::CCH - 1)));  // inverse of cslot
+    c_off[k] = 16 * (sl ^ (t & (CCH - 1))) + (PAGED ? t * ROWB : 0);
   }
 #pragma unroll
-  for (int k = 0; k < G::RL; ++k) {
-    const int q = 64 * k + lane, t = q / G::RCH, sl = q % G::RCH;
+  for (int k = 0; k < RLW; ++k) {
+    const int q = 64 * (RLW * wh + k) + lane, t = q / RCH, sl = q % RCH;
     r_tok[k] = t;
-    r_off[k] = 16 * (sl ^ (t & (G::RCH - 1)));
+    r_off[k] = 16 * (sl ^ (t & (RCH - 1))) + (PAGED ? t * G::RBYTES : 0);
   }
-  const bool p_live = lane < 32 * G::PCH;
-  const int p_tok = p_live ? lane / G::PCH : 0, p_off = p_live ? 16 * (lane % G::PCH) : 0;
+  // params: 2 PB chunks per tile, PB per wave (lanes < PB), not swizzled
+  const bool p_live = lane < PB;
+  const int p_tok = p_live ? (PB * wh + lane) / PCT : 0;
+  const int p_off = p_live ? 16 * ((PB * wh + lane) % PCT) + (PAGED ? p_tok * PB : 0) : 0;
 
-  // slot lookup for one tile: PAGED -> one page base; else per-lane token slots
-  struct Idx {
-    int base;
-    int cs[PAGED ? 1 : G::CL], rs[PAGED ? 1 : G::RL], ps;
-  };
-  auto lookup = [&](int tile, Idx& x) {
+  // positions are clamped into [0, L) as slot_of does; a tile never starts past L
+  const int pmask = (1 << sc.shift) - 1;
+  auto entry = [&](int pos) { return sc.idx[min(pos, L - 1) >> sc.shift]; };
+  auto slot = [&](int page, int pos) { return ((int64_t)page << sc.shift) + (min(pos, L - 1) & pmask); };
+  // PAGED: lane i holds the page of the pair's tile at step kb + i, so a step's
+  // page comes from a register (v_readlane) instead of a load and its wait
+  int pg_lane = 0;
+  auto lookup = [&](int step, Pages& x) {
+    const int tile = tile0 + kPairs * step;
     const int p0 = tile * TILE;
     if constexpr (PAGED) {
-      x.base = int(slot_of(sc, p0));
+      if ((step & 63) == 0) {
+        const int t = tile + kPairs * lane;
+        pg_lane = t < my_end ? entry(t * TILE) : 0;
+      }
+      x.pg = __builtin_amdgcn_readlane(pg_lane, step & 63);
     } else {
 #pragma unroll
-      for (int k = 0; k < G::CL; ++k) x.cs[k] = int(slot_of(sc, p0 + c_tok[k]));
+      for (int k = 0; k < CLW; ++k) x.cs[k] = entry(p0 + c_tok[k]);
 #pragma unroll
-      for (int k = 0; k < G::RL; ++k) x.rs[k] = int(slot_of(sc, p0 + r_tok[k]));
-      x.ps = int(slot_of(sc, p0 + p_tok));
+      for (int k = 0; k < RLW; ++k) x.rs[k] = entry(p0 + r_tok[k]);
+      x.ps = entry(p0 + p_tok);
     }
   };
-  auto dma = [&](const Idx& x, uint8_t* buf) {
-    if constexpr (PAGED) {
-      const uint8_t* cb = a.codes + (int64_t)x.base * ROWB;
-      const uint8_t* rb = reinterpret_cast<const uint8_t*>(a.rope) + (int64_t)x.base * G::RBYTES;
-      const uint8_t* pb = reinterpret_cast<const uint8_t*>(a.params) + (int64_t)x.base * PB;
-#pragma unroll
-      for (int k = 0; k < G::CL; ++k)
-        lds_dma16(cb + (c_tok[k] * ROWB + c_off[k]), buf + 1024 * k);
-#pragma unroll
-      for (int k = 0; k < G::RL; ++k)
-        lds_dma16(rb + (r_tok[k] * G::RBYTES + r_off[k]), buf + G::OFF_R + 1024 * k);
-      lds_dma16(pb + (p_tok * PB + p_off), buf + G::OFF_P);
-    } else {
-#pragma unroll
-      for (int k = 0; k < G::CL; ++k)
-        lds_dma16(a.codes + (int64_t)x.cs[k] * ROWB + c_off[k], buf + 1024 * k);
-#pragma unroll
-      for (int k = 0; k < G::RL; ++k)
-        lds_dma16(reinterpret_cast<const uint8_t*>(a.rope) + (int64_t)x.rs[k] * G::RBYTES + r_off[k],
-                  buf + G::OFF_R + 1024 * k);
-      lds_dma16(reinterpret_cast<const uint8_t*>(a.params) + (int64_t)x.ps * PB + p_off, buf + G::OFF_P);
-    }
-  };
-
-  auto compute = [&](int tile, const uint8_t* tl) {
+  auto dma = [&](int tile, const Pages& x, uint8_t* buf) {
     const int p0 = tile * TILE;
-    if ((p0 >= lo) && (p0 + TILE <= hi))
-      tile_compute<D, R, NHB, true>(st, tile, tl);
-    else
-      tile_compute<D, R, NHB, false>(st, tile, tl);
+    const uint8_t* rope8 = reinterpret_cast<const uint8_t*>(a.rope);
+    const uint8_t* par8 = reinterpret_cast<const uint8_t*>(a.params);
+    if constexpr (PAGED) {
+      const int64_t base = slot(x.pg, p0);
+      const uint8_t* cb = a.codes + base * ROWB;
+      const uint8_t* rb = rope8 + base * G::RBYTES;
+      const uint8_t* pb = par8 + base * PB;
+#pragma unroll
+      for (int k = 0; k < CLW; ++k) lds_dma16(cb + c_off[k], buf + 1024 * (CLW * wh + k));
+#pragma unroll
+      for (int k = 0; k < RLW; ++k) lds_dma16(rb + r_off[k], buf + G::OFF_R + 1024 * (RLW * wh + k));
+      if (p_live) lds_dma16(pb + p_off, buf + G::OFF_P + 16 * PB * wh);
+    } else {
+#pragma unroll
+      for (int k = 0; k < CLW; ++k)
+        lds_dma16(a.codes + slot(x.cs[k], p0 + c_tok[k]) * ROWB + c_off[k], buf + 1024 * (CLW * wh + k));
+#pragma unroll
+      for (int k = 0; k < RLW; ++k)
+        lds_dma16(rope8 + slot(x.rs[k], p0 + r_tok[k]) * G::RBYTES + r_off[k], buf + G::OFF_R + 1024 * (RLW * wh + k));
+      if (p_live) lds_dma16(par8 + slot(x.ps, p0 + p_tok) * PB + p_off, buf + G::OFF_P + 16 * PB * wh);
+    }
   };
 
-  // tiles of this wave: my_begin + wave + 4k
-  const int t0 = my_begin + wave;
-  const int nmine = t0 < my_end ? (my_end - t0 + 3) / 4 : 0;
-  Idx ix0, ix1, ix2;
-  if (nmine > 0) { lookup(t0, ix0); dma(ix0, tb0); }
-  if (nmine > 1) { lookup(t0 + 4, ix1); dma(ix1, tb1); }
-  if (nmine > 2) lookup(t0 + 8, ix2);
-  // step k computes tile k from ring buffer k % 3, after starting the DMA of
-  // tile k + 2 (its slots were looked up during step k - 1) and the lookup of k + 3
-  for (int k = 0; k < nmine; k += NBUF) {
-    if (k + 2 < nmine) dma(ix2, tb2);
-    if (k + 3 < nmine) lookup(t0 + 4 * (k + 3), ix0);
-    compute(t0 + 4 * k, tb0);
-    if (k + 1 >= nmine) break;
-    if (k + 3 < nmine) dma(ix0, tb0);
-    if (k + 4 < nmine) lookup(t0 + 4 * (k + 4), ix1);
-    compute(t0 + 4 * (k + 1), tb1);
-    if (k + 2 >= nmine) break;
-    if (k + 4 < nmine) dma(ix1, tb1);
-    if (k + 5 < nmine) lookup(t0 + 4 * (k + 5), ix2);
-    compute(t0 + 4 * (k + 2), tb2);
+  // ---- per-wave accumulators ---------------------------------------------------
+  f32x4 O[GW][8];   // output, groups GW wh + gg, N-block nbl: head 4gq + j, column la
+  f32x4 SP[GW];     // sum of p' per head (column 0)
+  float zp[GW];     // sum of p' * zero per head la (partial over this lane's tokens)
+  float l_lane;     // sum of p per head la (partial)
+  float m_ref = kNoRef, m_seen = kNoRef;
+
+  // phase 1: scores of tokens 16wh + (0..15) -> s_x[pr][par][wh]
+  auto phase1 = [&](int tile, uint8_t* tl, int par) {
+    const int p0 = tile * TILE;
+    const int tA = 16 * wh + la;  // A-operand token of this lane
+    uint32_t cw[2 * NG];          // words s = 2gq (cw[g]) and 2gq+1 (cw[NG+g]) of token tA
+    if constexpr (NG == 4) {
+      const u32x4 v0 = lds128(tl + 16 * G::cslot(tA, 2 * gq));
+      const u32x4 v1 = lds128(tl + 16 * G::cslot(tA, 2 * gq + 1));
+      cw[0] = v0.x; cw[1] = v0.y; cw[2] = v0.z; cw[3] = v0.w;
+      cw[4] = v1.x; cw[5] = v1.y; cw[6] = v1.z; cw[7] = v1.w;
+    } else {
+      const u32x4 v0 = lds128(tl + 16 * G::cslot(tA, gq));
+      cw[0] = v0.x; cw[1] = v0.y; cw[2] = v0.z; cw[3] = v0.w;
+    }
+    f32x4 accr = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kr = 0; kr < KR; ++kr)
+      accr = mfma16x16x32(lds128(tl + G::OFF_R + 16 * G::rslot(tA, 4 * kr + gq)), s_qr[kr][lane], accr);
+    float s[4] = {accr[0], accr[1], accr[2], accr[3]};
+    // C-layout tokens of this lane: 16wh + 4gq + j
+#pragma unroll
+    for (int gp = 0; gp < NG / 2; ++gp) {
+      f32x4 pv[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) pv[j] = lds128f(tl + G::OFF_P + (16 * wh + 4 * gq + j) * PB + 16 * gp);
+#pragma unroll
+      for (int gg = 0; gg < 2; ++gg) {
+        const int g = 2 * gp + gg;
+        uint32_t d0[8], d1[8];
+        unpack_word_fast(cw[g], d0, vbase);
+        unpack_word_fast(cw[NG + g], d1, vbase);
+        const u32x4 kop[4] = {{d0[0], d0[1], d0[2], d0[3]}, {d0[4], d0[5], d0[6], d0[7]},
+                              {d1[0], d1[1], d1[2], d1[3]}, {d1[4], d1[5], d1[6], d1[7]}};
+        const f32x2 qq = s_qq[g][la];  // Qsum, 4 Q' of head la
+        f32x4 acc = {-qq.y, -qq.y, -qq.y, -qq.y};
+#pragma unroll
+        for (int kbl = 0; kbl < 4; ++kbl) acc = mfma16x16x32(kop[kbl], s_qs[g][kbl][lane], acc);
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const float scl = gg ? pv[j].z : pv[j].x;
+          const float zr = gg ? pv[j].w : pv[j].y;
+          s[j] = fmaf(scl, fmaf(-zr, qq.x, acc[j]), s[j]);
+        }
+      }
+    }
+    const int pb = p0 + 16 * wh + 4 * gq;
+#pragma unroll
+    for (int j = 0; j < 4; ++j) s[j] = (pb + j >= lo && pb + j < hi) ? s[j] * scale_log2 : kNoRef;
+    s_x[pr][par][wh][lane] = f32x4{s[0], s[1], s[2], s[3]};
+    // params of masked tokens (rows that may never have been written) are
+    // zeroed for phase 2, so they contribute exactly 0 whatever they held
+    if (lane < PB) {
+      const int t = 16 * wh + lane / PCT, pos = p0 + t;
+      if (pos < lo || pos >= hi)
+        *reinterpret_cast<f32x4*>(tl + G::OFF_P + t * PB + 16 * (lane % PCT)) = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+  };
+
+  // phase 2: softmax of the tile and the output of groups GW wh .. GW wh + GW - 1
+  auto phase2 = [&](const uint8_t* tl, int par, bool first) {
+    const f32x4 x0 = s_x[pr][par][0][lane], x1 = s_x[pr][par][1][lane];
+    const float s[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};  // tokens tau(gq, i)
+    float lm = fmaxf(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])), fmaxf(fmaxf(s[4], s[5]), fmaxf(s[6], s[7])));
+    m_seen = fmaxf(m_seen, lm);
+    if (first) m_ref = wave_max_over_groups(lm);
+    float p[8], ls = 0.f;
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      p[i] = __builtin_amdgcn_exp2f(s[i] - m_ref);
+      ls += p[i];
+    }
+    l_lane += ls;
+    // tokens tau(gq, i) = 4gq + i (i < 4), 16 + 4gq + i - 4 (i >= 4)
+    float scl[GW][8], zr[GW][8];
+    uint32_t co[8][GW];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const int t = i < 4 ? 4 * gq + i : 16 + 4 * gq + (i - 4);
+      if constexpr (GW == 2) {
+        const f32x4 v = lds128f(tl + G::OFF_P + t * PB + 16 * wh);
+        scl[0][i] = v.x; zr[0][i] = v.y; scl[1][i] = v.z; zr[1][i] = v.w;
+        const u32x2 c = *reinterpret_cast<const u32x2*>(tl + 16 * G::cslot(t, la >> 1) + 8 * wh);
+        co[i][0] = c.x; co[i][1] = c.y;
+      } else {
+        const f32x2 v = *reinterpret_cast<const f32x2*>(tl + G::OFF_P + t * PB + 8 * wh);
+        scl[0][i] = v.x; zr[0][i] = v.y;
+        co[i][0] = *reinterpret_cast<const uint32_t*>(tl + 16 * G::cslot(t, la >> 2) + 8 * ((la >> 1) & 1) + 4 * wh);
+      }
+    }
+#pragma unroll
+    for (int gg = 0; gg < GW; ++gg) {
+      // p'_g = p * scale as a bf16 hi + lo pair: the two output MFMAs see
+      // hi + lo = p'_g to ~2^-17, so the contraction is FP32-accurate.
+      float pg[8];
+      float z = zp[gg];
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        pg[i] = p[i] * scl[gg][i];
+        z = fmaf(pg[i], zr[gg][i], z);
+      }
+      zp[gg] = z;
+      uint32_t hv[4], lv[4];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        hv[r] = pack_bf16(pg[2 * r], pg[2 * r + 1]);
+        lv[r] = pack_bf16(pg[2 * r] - bf16_lo(hv[r]), pg[2 * r + 1] - bf16_hi(hv[r]));
+      }
+      const u32x4 Ph = {hv[0], hv[1], hv[2], hv[3]}, Pl = {lv[0], lv[1], lv[2], lv[3]};
+      uint32_t dr[4][8];
+#pragma unroll
+      for (int r = 0; r < 4; ++r)
+        unpack_word_fast(__builtin_amdgcn_perm(co[2 * r + 1][gg], co[2 * r][gg], perm_sel), dr[r], vbase);
+#pragma unroll
+      for (int nbl = 0; nbl < 8; ++nbl) {
+        const u32x4 bv = {dr[0][nbl], dr[1][nbl], dr[2][nbl], dr[3][nbl]};
+        O[gg][nbl] = mfma16x16x32(Ph, bv, O[gg][nbl]);
+        O[gg][nbl] = mfma16x16x32(Pl, bv, O[gg][nbl]);
+      }
+      SP[gg] = mfma16x16x32(Ph, ones, SP[gg]);
+      SP[gg] = mfma16x16x32(Pl, ones, SP[gg]);
+    }
+  };
+
+  // ---- tile loop ---------------------------------------------------------------
+  uint8_t* const tb0 = s_r0 + pr * G::TILE_LDS;
+  uint8_t* const tb1 = s_r1 + pr * G::TILE_LDS;
+  uint8_t* const tb2 = s_r2 + pr * G::TILE_LDS;
+
+  for (int pass = 0; pass < 2; ++pass) {
+#pragma unroll
+    for (int gg = 0; gg < GW; ++gg) {
+#pragma unroll
+      for (int nbl = 0; nbl < 8; ++nbl) O[gg][nbl] = f32x4{0.f, 0.f, 0.f, 0.f};
+      SP[gg] = f32x4{0.f, 0.f, 0.f, 0.f};
+      zp[gg] = 0.f;
+    }
+    l_lane = 0.f;
+    m_seen = kNoRef;
+    Pages ix0, ix1, ix2;
+    if (nmine > 0) { lookup(0, ix0); dma(tile0, ix0, tb0); }
+    if (nmine > 1) { lookup(1, ix1); dma(tile0 + kPairs, ix1, tb1); }
+    if (nmine > 2) lookup(2, ix2);
+    __syncthreads();  // (waits for the loads above) tiles 0 and 1 are in LDS
+    // step k computes the pair's tile k from buffer k % 3; after its barrier it
+    // looks up the pages of tile k + 3 and loads tile k + 2 into buffer (k + 2) % 3
+#define ROLAQ_STEP(KK, CUR, NXT, IXN, IXL)                                         \
+    {                                                                              \
+      const int kk = (KK);                                                         \
+      const bool act = kk < nmine;                                                 \
+      if (act) phase1(tile0 + kPairs * kk, CUR, kk & 1);                           \
+      __syncthreads();                                                             \
+      if (kk + 3 < nmine) lookup(kk + 3, IXL);                                     \
+      if (kk + 2 < nmine) dma(tile0 + kPairs * (kk + 2), IXN, NXT);                \
+      if (act) phase2(CUR, kk & 1, pass == 0 && kk == 0);                          \
+    }
+    for (int k = 0; k < kmax; k += 3) {
+      ROLAQ_STEP(k, tb0, tb2, ix2, ix0)
+      if (k + 1 >= kmax) break;
+      ROLAQ_STEP(k + 1, tb1, tb0, ix0, ix1)
+      if (k + 2 >= kmax) break;
+      ROLAQ_STEP(k + 2, tb2, tb1, ix1, ix2)
+    }
+#undef ROLAQ_STEP
+    // a score above the reference by more than the slack: redo with the true max
+    const float m_true = wave_max_over_groups(m_seen);
+    const int redo = __syncthreads_or(pass == 0 && m_true > m_ref + kRefSlack);
+    if (!redo) break;
+    m_ref = m_true;
   }
 
-  // ---- finalize this wave: unnormalised o, m, l ------------------------------
+  // ---- merge the four pairs: unnormalised o, m, l --------------------------------
+  const float l_sum = wave_sum_over_groups(l_lane);
 #pragma unroll
-  for (int hb = 0; hb < NHB; ++hb) {
-    l_run[hb] = wave_sum_over_groups(l_run[hb]);
-#pragma unroll
-    for (int g = 0; g < NG; ++g) zp[hb][g] = wave_sum_over_groups(zp[hb][g]);
-    if (gq == 0) {
-      s_ml[wave][16 * hb + la][0] = m_run[hb];
-      s_ml[wave][16 * hb + la][1] = l_run[hb];
-    }
+  for (int gg = 0; gg < GW; ++gg) zp[gg] = wave_sum_over_groups(zp[gg]);
+  if (wh == 0 && gq == 0) {
+    s_ml[pr][la][0] = m_ref;
+    s_ml[pr][la][1] = l_sum;
   }
   __syncthreads();  // every wave is done with its tile buffers: s_r0 becomes the merge buffer
   float* s_obuf = reinterpret_cast<float*>(s_r0);
-  float fac[NHB][4];
+  float fac[4];
 #pragma unroll
-  for (int hb = 0; hb < NHB; ++hb)
+  for (int j = 0; j < 4; ++j) {
+    const int h = 4 * gq + j;
+    float M = kNoRef;
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int h = 16 * hb + 4 * gq + j;
-      float M = -1.0e30f;
+    for (int w = 0; w < kPairs; ++w) M = fmaxf(M, s_ml[w][h][0]);
+    float Ls = 0.f;
 #pragma unroll
-      for (int w = 0; w < 4; ++w) M = fmaxf(M, s_ml[w][h][0]);
-      float Ls = 0.f;
+    for (int w = 0; w < kPairs; ++w) Ls += __builtin_amdgcn_exp2f(s_ml[w][h][0] - M) * s_ml[w][h][1];
+    fac[j] = Ls > 0.f ? __builtin_amdgcn_exp2f(s_ml[pr][h][0] - M) / Ls : 0.f;
+  }
+  // pairs add their (disjoint-per-wave) features in a fixed order: deterministic
+  for (int w = 0; w < kPairs; ++w) {
+    if (pr == w) {
 #pragma unroll
-      for (int w = 0; w < 4; ++w) Ls += __builtin_amdgcn_exp2f(s_ml[w][h][0] - M) * s_ml[w][h][1];
-      fac[hb][j] = Ls > 0.f ? __builtin_amdgcn_exp2f(s_ml[wave][h][0] - M) / Ls : 0.f;
-    }
-  // one head block at a time: the four waves' partials are summed in a fixed
-  // order (deterministic) in s_obuf, then written out
+      for (int gg = 0; gg < GW; ++gg) {
+        const int g = GW * wh + gg;
+        float spo[4], zpo[4];
 #pragma unroll
-  for (int hb = 0; hb < NHB; ++hb) {
-    for (int w = 0; w < 4; ++w) {
-      if (wave == w) {
-        float spo[NG][4], zpo[NG][4];
+        for (int j = 0; j < 4; ++j) {
+          spo[j] = __shfl(SP[gg][j], 16 * gq);
+          zpo[j] = __shfl(zp[gg], 4 * gq + j);
+        }
 #pragma unroll
-        for (int g = 0; g < NG; ++g)
-#pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            spo[g][j] = __shfl(SP[hb][g][j], 16 * gq);
-            zpo[g][j] = __shfl(zp[hb][g], 4 * gq + j);
-          }
-#pragma unroll
-        for (int nb = 0; nb < NB; ++nb) {
-          const int g = nb / 8, nbl = nb % 8;
+        for (int nbl = 0; nbl < 8; ++nbl) {
           const int f = 128 * g + 16 * (la >> 1) + 8 * (la & 1) + nbl;
           const float wgt = pair_weight(nbl);
 #pragma unroll
           for (int j = 0; j < 4; ++j) {
-            const float v = ((O[hb][nb][j] - 4.f * spo[g][j]) * wgt - zpo[g][j]) * fac[hb][j];
+            const float v = ((O[gg][nbl][j] - 4.f * spo[j]) * wgt - zpo[j]) * fac[j];
             float* dst = &s_obuf[(4 * gq + j) * D + f];
             *dst = (w == 0) ? v : *dst + v;
           }
         }
       }
-      __syncthreads();
-    }
-    // write the head block's normalised partial
-    const int hmax = min(16, a.H - h0 - 16 * hb);
-    for (int e = tid; e < hmax * D; e += 256) {
-      const int h = e / D, f = e % D;
-      a.logits[(((int64_t)b * a.H + h0 + 16 * hb + h) * a.S1 + split) * D + f] = s_obuf[h * D + f];
     }
     __syncthreads();
   }
-  if (lane < 16 && wave < NHB) {
-    const int h = 16 * wave + lane;
-    if (h0 + h < a.H) {
-      float M = -1.0e30f;
-      for (int w = 0; w < 4; ++w) M = fmaxf(M, s_ml[w][h][0]);
-      float Ls = 0.f;
-      for (int w = 0; w < 4; ++w) Ls += __builtin_amdgcn_exp2f(s_ml[w][h][0] - M) * s_ml[w][h][1];
-      a.lse[((int64_t)b * a.H + h0 + h) * a.S1 + split] = Ls > 0.f ? (M + __log2f(Ls)) * kLn2 : kNeutralLse;
-    }
+  const int hmax = min(16, a.H - h0);
+  for (int e = tid; e < hmax * D; e += kThreads) {
+    const int h = e / D, f = e % D;
+    a.logits[(((int64_t)b * a.H + h0 + h) * a.S1 + split) * D + f] = s_obuf[h * D + f];
+  }
+  if (tid < hmax) {
+    const int h = tid;
+    float M = kNoRef;
+    for (int w = 0; w < kPairs; ++w) M = fmaxf(M, s_ml[w][h][0]);
+    float Ls = 0.f;
+    for (int w = 0; w < kPairs; ++w) Ls += __builtin_amdgcn_exp2f(s_ml[w][h][0] - M) * s_ml[w][h][1];
+    a.lse[((int64_t)b * a.H + h0 + h) * a.S1 + split] = Ls > 0.f ? (M + __log2f(Ls)) * kLn2 : kNeutralLse;
   }
 }
 
@@ -825,19 +701,19 @@ hipError_t rolaq_launch_decode(const rolaq::DecodeArgs& a, int D, int R, int max
                                uint16_t* out, int64_t o_sb, int64_t o_sh, hipStream_t stream) {
   using namespace rolaq;
   // one block per (sequence, 16 heads, split)
-  const dim3 grid(a.B * ((a.H + 15) / 16), max_splits + 1), block(256);
-#define ROLAQ_DEC(DD, RR, NH)                                                         \
-  if (D == DD && R == RR) {                                                           \
-    if (a.page_shift >= 5)                                                            \
-      hipLaunchKernelGGL((decode_stage1<DD, RR, NH, true>), grid, block, 0, stream, a);  \
-    else                                                                              \
-      hipLaunchKernelGGL((decode_stage1<DD, RR, NH, false>), grid, block, 0, stream, a); \
-    hipLaunchKernelGGL((decode_stage2<DD>), dim3(a.B * a.H), dim3(128), 0, stream,     \
-                       a.logits, a.lse, a.num_kv_splits, a.H, a.S1, out, o_sb, o_sh); \
-    return hipGetLastError();                                                         \
+  const dim3 grid(a.B * ((a.H + 15) / 16), max_splits + 1), block(kThreads);
+#define ROLAQ_DEC(DD, RR)                                                              \
+  if (D == DD && R == RR) {                                                            \
+    if (a.page_shift >= 5)                                                             \
+      hipLaunchKernelGGL((decode_stage1<DD, RR, true>), grid, block, 0, stream, a);    \
+    else                                                                               \
+      hipLaunchKernelGGL((decode_stage1<DD, RR, false>), grid, block, 0, stream, a);   \
+    hipLaunchKernelGGL((decode_stage2<DD>), dim3(a.B * a.H), dim3(128), 0, stream,      \
+                       a.logits, a.lse, a.num_kv_splits, a.H, a.S1, out, o_sb, o_sh);  \
+    return hipGetLastError();                                                          \
   }
-  ROLAQ_DEC(512, 64, 1)
-  ROLAQ_DEC(256, 32, 1)
+  ROLAQ_DEC(512, 64)
+  ROLAQ_DEC(256, 32)
 #undef ROLAQ_DEC
   return hipErrorInvalidValue;
 }
