@@ -107,13 +107,26 @@ __device__ void window_split(const DecodeArgs& a, int b, int h0, int slot_split,
 #pragma unroll
       for (int i = 0; i < RC; ++i) qr[i] = 0.f;
     }
+    static_assert(FC % 8 == 0 && (RC == 4 || RC == 2), "window chunking");
     for (int i = 0; i < nw; ++i) {
       const uint16_t* row = rows + i * ROWE;
       float acc = 0.f;
 #pragma unroll
-      for (int k = 0; k < FC; ++k) acc = fmaf(qv[k], bf16_to_float(row[c * FC + k]), acc);
-#pragma unroll
-      for (int k = 0; k < RC; ++k) acc = fmaf(qr[k], bf16_to_float(row[D + c * RC + k]), acc);
+      for (int k = 0; k < FC; k += 8) {
+        const u32x4 v = *reinterpret_cast<const u32x4*>(row + c * FC + k);
+        acc = fmaf(qv[k], bf16_lo(v.x), acc); acc = fmaf(qv[k + 1], bf16_hi(v.x), acc);
+        acc = fmaf(qv[k + 2], bf16_lo(v.y), acc); acc = fmaf(qv[k + 3], bf16_hi(v.y), acc);
+        acc = fmaf(qv[k + 4], bf16_lo(v.z), acc); acc = fmaf(qv[k + 5], bf16_hi(v.z), acc);
+        acc = fmaf(qv[k + 6], bf16_lo(v.w), acc); acc = fmaf(qv[k + 7], bf16_hi(v.w), acc);
+      }
+      if constexpr (RC == 4) {
+        const u32x2 v = *reinterpret_cast<const u32x2*>(row + D + c * RC);
+        acc = fmaf(qr[0], bf16_lo(v.x), acc); acc = fmaf(qr[1], bf16_hi(v.x), acc);
+        acc = fmaf(qr[2], bf16_lo(v.y), acc); acc = fmaf(qr[3], bf16_hi(v.y), acc);
+      } else {
+        const uint32_t v = *reinterpret_cast<const uint32_t*>(row + D + c * RC);
+        acc = fmaf(qr[0], bf16_lo(v), acc); acc = fmaf(qr[1], bf16_hi(v), acc);
+      }
       acc = wave_sum_over_groups(acc);  // chunks c, c^1, c^2, c^3 of this wave
       if (lane < 16) sc_part[(wave * 16 + h16) * MAXW + i] = acc;
     }
@@ -147,7 +160,13 @@ __device__ void window_split(const DecodeArgs& a, int b, int h0, int slot_split,
       const uint16_t* row = rows + i * ROWE;
       const float p = prob[h16 * MAXW + i];
 #pragma unroll
-      for (int k = 0; k < FC; ++k) o[k] = fmaf(p, bf16_to_float(row[c * FC + k]), o[k]);
+      for (int k = 0; k < FC; k += 8) {
+        const u32x4 v = *reinterpret_cast<const u32x4*>(row + c * FC + k);
+        o[k] = fmaf(p, bf16_lo(v.x), o[k]); o[k + 1] = fmaf(p, bf16_hi(v.x), o[k + 1]);
+        o[k + 2] = fmaf(p, bf16_lo(v.y), o[k + 2]); o[k + 3] = fmaf(p, bf16_hi(v.y), o[k + 3]);
+        o[k + 4] = fmaf(p, bf16_lo(v.z), o[k + 4]); o[k + 5] = fmaf(p, bf16_hi(v.z), o[k + 5]);
+        o[k + 6] = fmaf(p, bf16_lo(v.w), o[k + 6]); o[k + 7] = fmaf(p, bf16_hi(v.w), o[k + 7]);
+      }
     }
     if (hv) {
       float* dst = a.logits + (((int64_t)b * a.H + h) * a.S1 + slot_split) * D + c * FC;
@@ -200,10 +219,30 @@ __device__ __forceinline__ void unpack_word_fast(uint32_t w, uint32_t d[8], uint
 }
 
 // One 16-byte direct global->LDS load per lane (global_load_lds_dwordx4). The
-// LDS destination is wave-uniform: lane i lands at dst + 16 i.
+// LDS destination is wave-uniform: lane i lands at dst + 16 i. Issued as
+// inline asm, so the compiler adds no waits for it (it would otherwise wait
+// for every such load at the first LDS read after it): the caller orders reads
+// of the destination after the load with its own counted vmcnt wait. Nothing
+// else in these kernels uses m0.
 __device__ __forceinline__ void lds_dma16(const uint8_t* src, uint8_t* dst) {
-  typedef __attribute__((address_space(3))) void lds_t;
-  __builtin_amdgcn_global_load_lds(src, (lds_t*)dst, 16, 0, 0);
+  typedef __attribute__((address_space(3))) uint8_t lds8;
+  const uint32_t lds_addr = __builtin_amdgcn_readfirstlane(
+      static_cast<uint32_t>(reinterpret_cast<uintptr_t>((lds8*)dst)));
+  asm volatile("s_mov_b32 m0, %1\n\tglobal_load_lds_dwordx4 %0, off" ::"v"(src), "s"(lds_addr) : "memory");
+}
+
+// s_waitcnt immediates (gfx9 encoding): vmcnt <= n only / lgkmcnt == 0 only.
+constexpr int vmcnt_imm(int n) { return (n & 0xF) | ((n >> 4) << 14) | (0x7 << 4) | (0xF << 8); }
+constexpr int kLgkmcnt0 = 0xF | (0x3 << 14) | (0x7 << 4);
+
+// Workgroup barrier that waits for this wave's LDS operations only (not for
+// its global->LDS loads in flight); the empty asm statements keep the compiler
+// from moving memory operations across it.
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(kLgkmcnt0);
+  __builtin_amdgcn_s_barrier();
+  asm volatile("" ::: "memory");
 }
 
 // Page-table entries a wave needs for its share of one tile's direct loads:
@@ -304,53 +343,6 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
   const int tile0 = my_begin + pr;
   const int nmine = tile0 < my_end ? (my_end - tile0 + kPairs - 1) / kPairs : 0;
 
-  // ---- query operands (wave g < NG prepares group g) ---------------------------
-  // s_qs[g][kbl]: lane (gq, la) = head la, element pair r of K-block kbl <->
-  // in-group features 16s+k and 16s+k+8 with s = 2gq + kbl/2, k = 4(kbl%2) + r,
-  // scaled by 2^(5-e_k).
-  {
-    const int h = h0 + la;
-    const bool hv = h < a.H;
-    const uint16_t* qh = a.q + b * a.q_sb + (int64_t)min(h, a.H - 1) * a.q_sh;
-    if (wave < NG) {
-      const int g = wave;
-      float s_sum = 0.f, s_w = 0.f;
-#pragma unroll
-      for (int kbl = 0; kbl < 4; ++kbl) {
-        const int s = 2 * gq + kbl / 2;
-        const int f0 = 128 * g + 16 * s + 4 * (kbl % 2);
-        const u32x2 lo4 = *reinterpret_cast<const u32x2*>(qh + f0);
-        const u32x2 hi4 = *reinterpret_cast<const u32x2*>(qh + f0 + 8);
-        uint32_t outv[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const uint32_t wl = (r < 2 ? lo4.x : lo4.y), whi = (r < 2 ? hi4.x : hi4.y);
-          const float vl = hv ? ((r & 1) ? bf16_hi(wl) : bf16_lo(wl)) : 0.f;
-          const float vh = hv ? ((r & 1) ? bf16_hi(whi) : bf16_lo(whi)) : 0.f;
-          const float wk = pair_weight(4 * (kbl % 2) + r);
-          s_sum += vl + vh;
-          s_w += (vl + vh) * wk;
-          outv[r] = pack_bf16(vl * wk, vh * wk);
-        }
-        s_qs[g][kbl][lane] = u32x4{outv[0], outv[1], outv[2], outv[3]};
-      }
-      s_sum = wave_sum_over_groups(s_sum);
-      s_w = wave_sum_over_groups(s_w);
-      if (gq == 0) s_qq[g][la] = f32x2{s_sum, 4.f * s_w};
-    } else if (wave < NG + KR) {
-      // rope B operand of K-block kr: head la, dims 32kr + 8gq + i
-      const int kr = wave - NG;
-      const u32x4 v = *reinterpret_cast<const u32x4*>(qh + D + 32 * kr + 8 * gq);
-      s_qr[kr][lane] = hv ? v : u32x4{0, 0, 0, 0};
-    }
-  }
-  __syncthreads();
-  const uint32_t one = la == 0 ? 0x3F803F80u : 0u;
-  const u32x4 ones = {one, one, one, one};
-  const uint32_t perm_sel = (la & 1) ? 0x07060302u : 0x05040100u;
-  const uint32_t vbase = 0x40804080u;
-  const float scale_log2 = a.sm_scale * kLog2e;
-
   // ---- this wave's share of a tile's direct loads ------------------------------
   // load k of kind X moves chunk q = 64 (XLW wh + k) + lane to LDS slot q.
   int c_tok[CLW], c_off[CLW], r_tok[RLW], r_off[RLW];
@@ -419,6 +411,61 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
       if (p_live) lds_dma16(par8 + slot(x.ps, p0 + p_tok) * PB + p_off, buf + G::OFF_P + 16 * PB * wh);
     }
   };
+
+  uint8_t* const tb0 = s_r0 + pr * G::TILE_LDS;
+  uint8_t* const tb1 = s_r1 + pr * G::TILE_LDS;
+  uint8_t* const tb2 = s_r2 + pr * G::TILE_LDS;
+  // the first two tiles' loads fly while the query operands are prepared
+  Pages ix0, ix1, ix2;
+  if (nmine > 0) { lookup(0, ix0); dma(tile0, ix0, tb0); }
+  if (nmine > 1) { lookup(1, ix1); dma(tile0 + kPairs, ix1, tb1); }
+
+  // ---- query operands (wave g < NG prepares group g) ---------------------------
+  // s_qs[g][kbl]: lane (gq, la) = head la, element pair r of K-block kbl <->
+  // in-group features 16s+k and 16s+k+8 with s = 2gq + kbl/2, k = 4(kbl%2) + r,
+  // scaled by 2^(5-e_k).
+  {
+    const int h = h0 + la;
+    const bool hv = h < a.H;
+    const uint16_t* qh = a.q + b * a.q_sb + (int64_t)min(h, a.H - 1) * a.q_sh;
+    if (wave < NG) {
+      const int g = wave;
+      float s_sum = 0.f, s_w = 0.f;
+#pragma unroll
+      for (int kbl = 0; kbl < 4; ++kbl) {
+        const int s = 2 * gq + kbl / 2;
+        const int f0 = 128 * g + 16 * s + 4 * (kbl % 2);
+        const u32x2 lo4 = *reinterpret_cast<const u32x2*>(qh + f0);
+        const u32x2 hi4 = *reinterpret_cast<const u32x2*>(qh + f0 + 8);
+        uint32_t outv[4];
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+          const uint32_t wl = (r < 2 ? lo4.x : lo4.y), whi = (r < 2 ? hi4.x : hi4.y);
+          const float vl = hv ? ((r & 1) ? bf16_hi(wl) : bf16_lo(wl)) : 0.f;
+          const float vh = hv ? ((r & 1) ? bf16_hi(whi) : bf16_lo(whi)) : 0.f;
+          const float wk = pair_weight(4 * (kbl % 2) + r);
+          s_sum += vl + vh;
+          s_w += (vl + vh) * wk;
+          outv[r] = pack_bf16(vl * wk, vh * wk);
+        }
+        s_qs[g][kbl][lane] = u32x4{outv[0], outv[1], outv[2], outv[3]};
+      }
+      s_sum = wave_sum_over_groups(s_sum);
+      s_w = wave_sum_over_groups(s_w);
+      if (gq == 0) s_qq[g][la] = f32x2{s_sum, 4.f * s_w};
+    } else if (wave < NG + KR) {
+      // rope B operand of K-block kr: head la, dims 32kr + 8gq + i
+      const int kr = wave - NG;
+      const u32x4 v = *reinterpret_cast<const u32x4*>(qh + D + 32 * kr + 8 * gq);
+      s_qr[kr][lane] = hv ? v : u32x4{0, 0, 0, 0};
+    }
+  }
+  lds_barrier();
+  const uint32_t one = la == 0 ? 0x3F803F80u : 0u;
+  const u32x4 ones = {one, one, one, one};
+  const uint32_t perm_sel = (la & 1) ? 0x07060302u : 0x05040100u;
+  const uint32_t vbase = 0x40804080u;
+  const float scale_log2 = a.sm_scale * kLog2e;
 
   // ---- per-wave accumulators ---------------------------------------------------
   f32x4 O[GW][8];   // output, groups GW wh + gg, N-block nbl: head 4gq + j, column la
@@ -551,9 +598,6 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
   };
 
   // ---- tile loop ---------------------------------------------------------------
-  uint8_t* const tb0 = s_r0 + pr * G::TILE_LDS;
-  uint8_t* const tb1 = s_r1 + pr * G::TILE_LDS;
-  uint8_t* const tb2 = s_r2 + pr * G::TILE_LDS;
 
   for (int pass = 0; pass < 2; ++pass) {
 #pragma unroll
@@ -565,19 +609,30 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
     }
     l_lane = 0.f;
     m_seen = kNoRef;
-    Pages ix0, ix1, ix2;
-    if (nmine > 0) { lookup(0, ix0); dma(tile0, ix0, tb0); }
-    if (nmine > 1) { lookup(1, ix1); dma(tile0 + kPairs, ix1, tb1); }
+    if (pass > 0) {
+      if (nmine > 0) { lookup(0, ix0); dma(tile0, ix0, tb0); }
+      if (nmine > 1) { lookup(1, ix1); dma(tile0 + kPairs, ix1, tb1); }
+    }
     if (nmine > 2) lookup(2, ix2);
-    __syncthreads();  // (waits for the loads above) tiles 0 and 1 are in LDS
-    // step k computes the pair's tile k from buffer k % 3; after its barrier it
-    // looks up the pages of tile k + 3 and loads tile k + 2 into buffer (k + 2) % 3
+    // Step k computes the pair's tile k from buffer k % 3. Each wave loads the
+    // rows of its own 16 tokens, waits for them itself (the loads issued after
+    // those of tile k are the page lookups of tile k + 2 and the loads of tile
+    // k + 1, at least kDmaW memory ops, so vmcnt <= kDmaW completes tile k), and
+    // reads its partner's rows only after the barrier that follows the
+    // partner's own wait. After the barrier it looks up the pages of tile k + 3
+    // and loads tile k + 2 into buffer (k + 2) % 3, which both waves finished
+    // reading before that barrier.
+    constexpr int kDmaW = CLW + RLW + 1;
 #define ROLAQ_STEP(KK, CUR, NXT, IXN, IXL)                                         \
     {                                                                              \
       const int kk = (KK);                                                         \
       const bool act = kk < nmine;                                                 \
+      if (kk + 1 < nmine)                                                          \
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(kDmaW));                              \
+      else                                                                         \
+        __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));                                  \
       if (act) phase1(tile0 + kPairs * kk, CUR, kk & 1);                           \
-      __syncthreads();                                                             \
+      lds_barrier();                                                               \
       if (kk + 3 < nmine) lookup(kk + 3, IXL);                                     \
       if (kk + 2 < nmine) dma(tile0 + kPairs * (kk + 2), IXN, NXT);                \
       if (act) phase2(CUR, kk & 1, pass == 0 && kk == 0);                          \
@@ -605,8 +660,7 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
     s_ml[pr][la][0] = m_ref;
     s_ml[pr][la][1] = l_sum;
   }
-  __syncthreads();  // every wave is done with its tile buffers: s_r0 becomes the merge buffer
-  float* s_obuf = reinterpret_cast<float*>(s_r0);
+  __syncthreads();  // every wave is done with its tile buffers
   float fac[4];
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
@@ -619,37 +673,74 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
     for (int w = 0; w < kPairs; ++w) Ls += __builtin_amdgcn_exp2f(s_ml[w][h][0] - M) * s_ml[w][h][1];
     fac[j] = Ls > 0.f ? __builtin_amdgcn_exp2f(s_ml[pr][h][0] - M) / Ls : 0.f;
   }
-  // pairs add their (disjoint-per-wave) features in a fixed order: deterministic
-  for (int w = 0; w < kPairs; ++w) {
-    if (pr == w) {
+  // this wave's partial o = ((O - 4 SP) 2^(5-e) - ZP) * fac for its groups, in place
 #pragma unroll
-      for (int gg = 0; gg < GW; ++gg) {
-        const int g = GW * wh + gg;
-        float spo[4], zpo[4];
+  for (int gg = 0; gg < GW; ++gg) {
+    float spo[4], zpo[4];
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          spo[j] = __shfl(SP[gg][j], 16 * gq);
-          zpo[j] = __shfl(zp[gg], 4 * gq + j);
-        }
+    for (int j = 0; j < 4; ++j) {
+      spo[j] = __shfl(SP[gg][j], 16 * gq);
+      zpo[j] = __shfl(zp[gg], 4 * gq + j);
+    }
 #pragma unroll
-        for (int nbl = 0; nbl < 8; ++nbl) {
-          const int f = 128 * g + 16 * (la >> 1) + 8 * (la & 1) + nbl;
-          const float wgt = pair_weight(nbl);
+    for (int nbl = 0; nbl < 8; ++nbl) {
+      const float wgt = pair_weight(nbl);
 #pragma unroll
-          for (int j = 0; j < 4; ++j) {
-            const float v = ((O[gg][nbl][j] - 4.f * spo[j]) * wgt - zpo[j]) * fac[j];
-            float* dst = &s_obuf[(4 * gq + j) * D + f];
-            *dst = (w == 0) ? v : *dst + v;
-          }
-        }
+      for (int j = 0; j < 4; ++j) O[gg][nbl][j] = ((O[gg][nbl][j] - 4.f * spo[j]) * wgt - zpo[j]) * fac[j];
+    }
+  }
+  // fixed-order sum over the pairs ((p0 + p1) + (p2 + p3)) through LDS in the
+  // accumulator layout [wave of pair][group][N-block][lane]: plain stores and
+  // loads, no read-modify-write chains
+  auto slot4 = [&](int gg, int nbl) { return ((wh * GW + gg) * 8 + nbl) * 64 + lane; };
+  f32x4* xb0 = reinterpret_cast<f32x4*>(s_r0);
+  f32x4* xb1 = reinterpret_cast<f32x4*>(s_r1);
+  f32x4* xb2 = reinterpret_cast<f32x4*>(s_r2);
+  static_assert(2 * GW * 8 * 64 * 16 <= RING, "partial buffer");
+  if (pr == 1 || pr == 3) {
+    f32x4* dst = pr == 1 ? xb0 : xb1;
+#pragma unroll
+    for (int gg = 0; gg < GW; ++gg)
+#pragma unroll
+      for (int nbl = 0; nbl < 8; ++nbl) dst[slot4(gg, nbl)] = O[gg][nbl];
+  }
+  __syncthreads();
+  if (pr == 0 || pr == 2) {
+    const f32x4* src = pr == 0 ? xb0 : xb1;
+#pragma unroll
+    for (int gg = 0; gg < GW; ++gg)
+#pragma unroll
+      for (int nbl = 0; nbl < 8; ++nbl) O[gg][nbl] += src[slot4(gg, nbl)];
+  }
+  if (pr == 2) {
+#pragma unroll
+    for (int gg = 0; gg < GW; ++gg)
+#pragma unroll
+      for (int nbl = 0; nbl < 8; ++nbl) xb2[slot4(gg, nbl)] = O[gg][nbl];
+  }
+  __syncthreads();
+  // pair 0 finishes the sum and scatters it to s_obuf[head][feature] (in s_r0,
+  // whose partials it has already consumed)
+  float* s_obuf = reinterpret_cast<float*>(s_r0);
+  if (pr == 0) {
+#pragma unroll
+    for (int gg = 0; gg < GW; ++gg) {
+      const int g = GW * wh + gg;
+#pragma unroll
+      for (int nbl = 0; nbl < 8; ++nbl) {
+        const f32x4 v = O[gg][nbl] + xb2[slot4(gg, nbl)];
+        const int f = 128 * g + 16 * (la >> 1) + 8 * (la & 1) + nbl;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) s_obuf[(4 * gq + j) * D + f] = v[j];
       }
     }
-    __syncthreads();
   }
+  __syncthreads();
   const int hmax = min(16, a.H - h0);
-  for (int e = tid; e < hmax * D; e += kThreads) {
+  for (int e = 4 * tid; e < hmax * D; e += 4 * kThreads) {
     const int h = e / D, f = e % D;
-    a.logits[(((int64_t)b * a.H + h0 + h) * a.S1 + split) * D + f] = s_obuf[h * D + f];
+    *reinterpret_cast<f32x4*>(&a.logits[(((int64_t)b * a.H + h0 + h) * a.S1 + split) * D + f]) =
+        *reinterpret_cast<const f32x4*>(&s_obuf[h * D + f]);
   }
   if (tid < hmax) {
     const int h = tid;
