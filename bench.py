@@ -261,7 +261,7 @@ def main():
     db = DecodeBench(args.layers, dev)
     print(f"[bench] decode caches written for {args.layers} layers in {time.time() - t_setup:.1f}s", file=sys.stderr,
           flush=True)
-    candidates = [args.splits] if args.splits else [5, 8, 9, 17, 33]
+    candidates = [args.splits] if args.splits else [8, 9, 15, 16, 17, 33]
     best = None
     for ns in candidates:
         db.alloc_scratch(ns)

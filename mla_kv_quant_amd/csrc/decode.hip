@@ -59,12 +59,11 @@ __device__ __forceinline__ f32x4 lds128f(const uint8_t* p) { return *reinterpret
 // ---------------------------------------------------------------------------
 constexpr int kMaxWindow = 32;
 template <int D, int R>
-constexpr int window_rows_bytes() { return kMaxWindow * (D + R) * 2; }
-constexpr int window_part_floats() { return (4 * 16 + 16) * kMaxWindow + 16; }
+constexpr int window_half_rows_bytes() { return kMaxWindow / 2 * (D + R) * 2; }
 
 template <int D, int R>
 __device__ void window_split(const DecodeArgs& a, int b, int h0, int slot_split, const SeqCtx& sc,
-                             int64_t req, float* smem, uint8_t* rows_mem) {
+                             int64_t req, float* sc_part, float* prob, uint8_t* rows_lo, uint8_t* rows_hi) {
   constexpr int MAXW = kMaxWindow;
   constexpr int FC = D / 16, RC = R / 16;
   constexpr int ROWE = D + R;  // staged row: latent | rope (bf16 elements)
@@ -75,9 +74,11 @@ __device__ void window_split(const DecodeArgs& a, int b, int h0, int slot_split,
   const int n_sink = min(P, L);
   const int rec_lo = max(L - W, n_sink);
   const int nw = n_sink + (L - rec_lo);
-  uint16_t* rows = reinterpret_cast<uint16_t*>(rows_mem);             // [MAXW][ROWE]
-  float* sc_part = smem;                                              // [4 waves][16][MAXW]
-  float* prob = sc_part + 4 * 16 * MAXW;                              // [16][MAXW] + 16
+  // staged rows [MAXW][ROWE]: rows 0-15 in rows_lo, 16-31 in rows_hi
+  auto row_at = [&](int i) {
+    return reinterpret_cast<uint16_t*>(i < MAXW / 2 ? rows_lo : rows_hi) + (i & (MAXW / 2 - 1)) * ROWE;
+  };
+  // sc_part: [4 waves][16][MAXW]; prob: [16][MAXW] + 16
   // stage rows: D/8 + R/8 16-byte chunks per row
   constexpr int CPR = (D + R) / 8;
   for (int k = t; k < nw * CPR; k += blockDim.x) {
@@ -85,7 +86,7 @@ __device__ void window_split(const DecodeArgs& a, int b, int h0, int slot_split,
     const int pos = i < n_sink ? i : rec_lo + (i - n_sink);
     const uint16_t* src = ch < D / 8 ? a.hp + (int64_t)ring_row(req, pos, P, W) * D + 8 * ch
                                      : a.rope + slot_of(sc, pos) * R + 8 * (ch - D / 8);
-    *reinterpret_cast<u32x4*>(rows + i * ROWE + 8 * ch) = *reinterpret_cast<const u32x4*>(src);
+    *reinterpret_cast<u32x4*>(row_at(i) + 8 * ch) = *reinterpret_cast<const u32x4*>(src);
   }
   __syncthreads();
   const int h = h0 + h16;
@@ -109,7 +110,7 @@ __device__ void window_split(const DecodeArgs& a, int b, int h0, int slot_split,
     }
     static_assert(FC % 8 == 0 && (RC == 4 || RC == 2), "window chunking");
     for (int i = 0; i < nw; ++i) {
-      const uint16_t* row = rows + i * ROWE;
+      const uint16_t* row = row_at(i);
       float acc = 0.f;
 #pragma unroll
       for (int k = 0; k < FC; k += 8) {
@@ -157,7 +158,7 @@ __device__ void window_split(const DecodeArgs& a, int b, int h0, int slot_split,
 #pragma unroll
     for (int k = 0; k < FC; ++k) o[k] = 0.f;
     for (int i = 0; i < nw; ++i) {
-      const uint16_t* row = rows + i * ROWE;
+      const uint16_t* row = row_at(i);
       const float p = prob[h16 * MAXW + i];
 #pragma unroll
       for (int k = 0; k < FC; k += 8) {
@@ -255,8 +256,8 @@ struct TilePages {
   int cs[PAGED ? 1 : CLW], rs[PAGED ? 1 : RLW], ps;
 };
 
-constexpr int kPairs = 4;                // wave pairs per block
-constexpr int kThreads = 128 * kPairs;   // 8 waves
+constexpr int kPairs = 2;                // wave pairs per block
+constexpr int kThreads = 128 * kPairs;   // 4 waves; two blocks share a CU
 constexpr float kNoRef = -1.0e30f;       // "no score yet" / masked score (log2 units)
 constexpr float kRefSlack = 64.f;        // max exp2 argument before a split is redone
 
@@ -282,7 +283,7 @@ constexpr float kRefSlack = 64.f;        // max exp2 argument before a split is 
 // recomputed with the true max, so the tile loop carries no rescaling.
 // ---------------------------------------------------------------------------
 template <int D, int R, bool PAGED>
-__global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
+__global__ __launch_bounds__(kThreads, 2) void decode_stage1(DecodeArgs a) {
   using G = Geo<D, R>;
   constexpr int NG = G::NG, KR = G::KR, ROWB = G::ROWB, PB = G::PB, CCH = G::CCH, RCH = G::RCH;
   constexpr int GW = NG / 2;                  // output groups per wave
@@ -291,8 +292,9 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
   constexpr int TILE = 32;
   constexpr int RING = kPairs * G::TILE_LDS;
   static_assert(R % 32 == 0 && D % 256 == 0, "unsupported shape");
-  static_assert(16 * D * 4 <= RING, "merge buffer does not fit in one ring buffer");
-  static_assert(window_rows_bytes<D, R>() <= RING && window_part_floats() * 4 <= RING, "window scratch");
+  static_assert(8 * D * 4 <= RING, "merge buffer (8 heads) does not fit in one ring buffer");
+  static_assert(window_half_rows_bytes<D, R>() <= RING && 4 * 16 * kMaxWindow * 4 <= RING &&
+                (16 * kMaxWindow + 16) * 4 <= NG * 4 * 64 * 16, "window scratch");
   using Pages = TilePages<CLW, RLW, PAGED>;
 
   // Three tile buffers as separate LDS objects, so the compiler's wait
@@ -300,7 +302,6 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t s_r0[RING];
   __shared__ __attribute__((aligned(16))) uint8_t s_r1[RING];
   __shared__ __attribute__((aligned(16))) uint8_t s_r2[RING];
-  __shared__ f32x4 s_x[kPairs][2][2][64];  // phase-1 scores [pair][step parity][wave of pair][lane]
   // score-MFMA B operands of the query: [group][K-block][lane]
   __shared__ __attribute__((aligned(16))) u32x4 s_qs[NG][4][64];
   __shared__ __attribute__((aligned(16))) u32x4 s_qr[KR][64];  // rope B operands
@@ -321,7 +322,8 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
   const int64_t req = a.req_idx[b];
 
   if (split == nq) {
-    window_split<D, R>(a, b, h0, split, sc, req, reinterpret_cast<float*>(s_r0), s_r1);
+    window_split<D, R>(a, b, h0, split, sc, req, reinterpret_cast<float*>(s_r2),
+                       reinterpret_cast<float*>(&s_qs[0][0][0]), s_r0, s_r1);
     return;
   }
 
@@ -420,29 +422,37 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
   if (nmine > 0) { lookup(0, ix0); dma(tile0, ix0, tb0); }
   if (nmine > 1) { lookup(1, ix1); dma(tile0 + kPairs, ix1, tb1); }
 
-  // ---- query operands (wave g < NG prepares group g) ---------------------------
+  // ---- query operands (wave w prepares groups w, w + 4, .. and rope K-block w) ---
   // s_qs[g][kbl]: lane (gq, la) = head la, element pair r of K-block kbl <->
   // in-group features 16s+k and 16s+k+8 with s = 2gq + kbl/2, k = 4(kbl%2) + r,
-  // scaled by 2^(5-e_k).
+  // scaled by 2^(5-e_k). The lane reads its 32 features 32gq.. of the group
+  // with four 16-byte loads.
   {
     const int h = h0 + la;
     const bool hv = h < a.H;
     const uint16_t* qh = a.q + b * a.q_sb + (int64_t)min(h, a.H - 1) * a.q_sh;
-    if (wave < NG) {
-      const int g = wave;
+    if (wave < KR) {
+      // rope B operand of K-block kr: head la, dims 32kr + 8gq + i
+      const u32x4 v = *reinterpret_cast<const u32x4*>(qh + D + 32 * wave + 8 * gq);
+      s_qr[wave][lane] = hv ? v : u32x4{0, 0, 0, 0};
+    }
+    for (int g = wave; g < NG; g += 2 * kPairs) {
+      u32x4 v[4];  // features 128g + 32gq + 8i .. +7
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const u32x4 x = *reinterpret_cast<const u32x4*>(qh + 128 * g + 32 * gq + 8 * i);
+        v[i] = hv ? x : u32x4{0, 0, 0, 0};
+      }
       float s_sum = 0.f, s_w = 0.f;
 #pragma unroll
       for (int kbl = 0; kbl < 4; ++kbl) {
-        const int s = 2 * gq + kbl / 2;
-        const int f0 = 128 * g + 16 * s + 4 * (kbl % 2);
-        const u32x2 lo4 = *reinterpret_cast<const u32x2*>(qh + f0);
-        const u32x2 hi4 = *reinterpret_cast<const u32x2*>(qh + f0 + 8);
+        const u32x4 vlo = v[2 * (kbl / 2)], vhi = v[2 * (kbl / 2) + 1];  // k and k + 8
         uint32_t outv[4];
 #pragma unroll
         for (int r = 0; r < 4; ++r) {
-          const uint32_t wl = (r < 2 ? lo4.x : lo4.y), whi = (r < 2 ? hi4.x : hi4.y);
-          const float vl = hv ? ((r & 1) ? bf16_hi(wl) : bf16_lo(wl)) : 0.f;
-          const float vh = hv ? ((r & 1) ? bf16_hi(whi) : bf16_lo(whi)) : 0.f;
+          const int d = 2 * (kbl % 2) + r / 2;  // dword of element 4(kbl%2) + r
+          const float vl = (r & 1) ? bf16_hi(vlo[d]) : bf16_lo(vlo[d]);
+          const float vh = (r & 1) ? bf16_hi(vhi[d]) : bf16_lo(vhi[d]);
           const float wk = pair_weight(4 * (kbl % 2) + r);
           s_sum += vl + vh;
           s_w += (vl + vh) * wk;
@@ -453,11 +463,6 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
       s_sum = wave_sum_over_groups(s_sum);
       s_w = wave_sum_over_groups(s_w);
       if (gq == 0) s_qq[g][la] = f32x2{s_sum, 4.f * s_w};
-    } else if (wave < NG + KR) {
-      // rope B operand of K-block kr: head la, dims 32kr + 8gq + i
-      const int kr = wave - NG;
-      const u32x4 v = *reinterpret_cast<const u32x4*>(qh + D + 32 * kr + 8 * gq);
-      s_qr[kr][lane] = hv ? v : u32x4{0, 0, 0, 0};
     }
   }
   lds_barrier();
@@ -474,8 +479,9 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
   float l_lane;     // sum of p per head la (partial)
   float m_ref = kNoRef, m_seen = kNoRef;
 
-  // phase 1: scores of tokens 16wh + (0..15) -> s_x[pr][par][wh]
-  auto phase1 = [&](int tile, uint8_t* tl, int par) {
+  // phase 1: scores of tokens 16wh + (0..15), left for the partner in this
+  // wave's own (now consumed) rope rows of the tile buffer
+  auto phase1 = [&](int tile, uint8_t* tl) {
     const int p0 = tile * TILE;
     const int tA = 16 * wh + la;  // A-operand token of this lane
     uint32_t cw[2 * NG];          // words s = 2gq (cw[g]) and 2gq+1 (cw[NG+g]) of token tA
@@ -522,7 +528,7 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
     const int pb = p0 + 16 * wh + 4 * gq;
 #pragma unroll
     for (int j = 0; j < 4; ++j) s[j] = (pb + j >= lo && pb + j < hi) ? s[j] * scale_log2 : kNoRef;
-    s_x[pr][par][wh][lane] = f32x4{s[0], s[1], s[2], s[3]};
+    *reinterpret_cast<f32x4*>(tl + G::OFF_R + 16 * G::RBYTES * wh + 16 * lane) = f32x4{s[0], s[1], s[2], s[3]};
     // params of masked tokens (rows that may never have been written) are
     // zeroed for phase 2, so they contribute exactly 0 whatever they held
     if (lane < PB) {
@@ -533,8 +539,9 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
   };
 
   // phase 2: softmax of the tile and the output of groups GW wh .. GW wh + GW - 1
-  auto phase2 = [&](const uint8_t* tl, int par, bool first) {
-    const f32x4 x0 = s_x[pr][par][0][lane], x1 = s_x[pr][par][1][lane];
+  auto phase2 = [&](const uint8_t* tl, bool first) {
+    const f32x4 x0 = *reinterpret_cast<const f32x4*>(tl + G::OFF_R + 16 * lane);
+    const f32x4 x1 = *reinterpret_cast<const f32x4*>(tl + G::OFF_R + 16 * G::RBYTES + 16 * lane);
     const float s[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};  // tokens tau(gq, i)
     float lm = fmaxf(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])), fmaxf(fmaxf(s[4], s[5]), fmaxf(s[6], s[7])));
     m_seen = fmaxf(m_seen, lm);
@@ -631,11 +638,11 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
         __builtin_amdgcn_s_waitcnt(vmcnt_imm(kDmaW));                              \
       else                                                                         \
         __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));                                  \
-      if (act) phase1(tile0 + kPairs * kk, CUR, kk & 1);                           \
+      if (act) phase1(tile0 + kPairs * kk, CUR);                                   \
       lds_barrier();                                                               \
       if (kk + 3 < nmine) lookup(kk + 3, IXL);                                     \
       if (kk + 2 < nmine) dma(tile0 + kPairs * (kk + 2), IXN, NXT);                \
-      if (act) phase2(CUR, kk & 1, pass == 0 && kk == 0);                          \
+      if (act) phase2(CUR, pass == 0 && kk == 0);                                  \
     }
     for (int k = 0; k < kmax; k += 3) {
       ROLAQ_STEP(k, tb0, tb2, ix2, ix0)
@@ -652,7 +659,7 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
     m_ref = m_true;
   }
 
-  // ---- merge the four pairs: unnormalised o, m, l --------------------------------
+  // ---- merge the pairs: unnormalised o, m, l --------------------------------
   const float l_sum = wave_sum_over_groups(l_lane);
 #pragma unroll
   for (int gg = 0; gg < GW; ++gg) zp[gg] = wave_sum_over_groups(zp[gg]);
@@ -689,49 +696,37 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
       for (int j = 0; j < 4; ++j) O[gg][nbl][j] = ((O[gg][nbl][j] - 4.f * spo[j]) * wgt - zpo[j]) * fac[j];
     }
   }
-  // fixed-order sum over the pairs ((p0 + p1) + (p2 + p3)) through LDS in the
-  // accumulator layout [wave of pair][group][N-block][lane]: plain stores and
-  // loads, no read-modify-write chains
-  auto slot4 = [&](int gg, int nbl) { return ((wh * GW + gg) * 8 + nbl) * 64 + lane; };
-  f32x4* xb0 = reinterpret_cast<f32x4*>(s_r0);
-  f32x4* xb1 = reinterpret_cast<f32x4*>(s_r1);
-  f32x4* xb2 = reinterpret_cast<f32x4*>(s_r2);
-  static_assert(2 * GW * 8 * 64 * 16 <= RING, "partial buffer");
-  if (pr == 1 || pr == 3) {
-    f32x4* dst = pr == 1 ? xb0 : xb1;
+  // pair 1 hands its partials to pair 0 through LDS in the accumulator layout
+  // (wave wh of the pair through buffer wh): plain stores and loads, no
+  // read-modify-write chains; pair 0 adds them (p0 + p1, a fixed order)
+  static_assert(kPairs == 2, "the merge below is written for two pairs");
+  static_assert(GW * 8 * 64 * 16 <= RING, "partial buffer");
+  f32x4* xb = reinterpret_cast<f32x4*>(wh == 0 ? s_r0 : s_r1);
+  auto slot4 = [&](int gg, int nbl) { return (gg * 8 + nbl) * 64 + lane; };
+  if (pr == 1) {
 #pragma unroll
     for (int gg = 0; gg < GW; ++gg)
 #pragma unroll
-      for (int nbl = 0; nbl < 8; ++nbl) dst[slot4(gg, nbl)] = O[gg][nbl];
+      for (int nbl = 0; nbl < 8; ++nbl) xb[slot4(gg, nbl)] = O[gg][nbl];
   }
   __syncthreads();
-  if (pr == 0 || pr == 2) {
-    const f32x4* src = pr == 0 ? xb0 : xb1;
+  if (pr == 0) {
 #pragma unroll
     for (int gg = 0; gg < GW; ++gg)
 #pragma unroll
-      for (int nbl = 0; nbl < 8; ++nbl) O[gg][nbl] += src[slot4(gg, nbl)];
+      for (int nbl = 0; nbl < 8; ++nbl) O[gg][nbl] += xb[slot4(gg, nbl)];
   }
-  if (pr == 2) {
-#pragma unroll
-    for (int gg = 0; gg < GW; ++gg)
-#pragma unroll
-      for (int nbl = 0; nbl < 8; ++nbl) xb2[slot4(gg, nbl)] = O[gg][nbl];
-  }
-  __syncthreads();
-  // pair 0 finishes the sum and scatters it to s_obuf[head][feature] (in s_r0,
-  // whose partials it has already consumed)
-  float* s_obuf = reinterpret_cast<float*>(s_r0);
+  __syncthreads();  // partials consumed: s_r2 / s_r0 take heads 0-7 / 8-15
+  auto obuf = [&](int h) { return reinterpret_cast<float*>(h < 8 ? s_r2 : s_r0) + (h & 7) * D; };
   if (pr == 0) {
 #pragma unroll
     for (int gg = 0; gg < GW; ++gg) {
       const int g = GW * wh + gg;
 #pragma unroll
       for (int nbl = 0; nbl < 8; ++nbl) {
-        const f32x4 v = O[gg][nbl] + xb2[slot4(gg, nbl)];
         const int f = 128 * g + 16 * (la >> 1) + 8 * (la & 1) + nbl;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) s_obuf[(4 * gq + j) * D + f] = v[j];
+        for (int j = 0; j < 4; ++j) obuf(4 * gq + j)[f] = O[gg][nbl][j];
       }
     }
   }
@@ -740,7 +735,7 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
   for (int e = 4 * tid; e < hmax * D; e += 4 * kThreads) {
     const int h = e / D, f = e % D;
     *reinterpret_cast<f32x4*>(&a.logits[(((int64_t)b * a.H + h0 + h) * a.S1 + split) * D + f]) =
-        *reinterpret_cast<const f32x4*>(&s_obuf[h * D + f]);
+        *reinterpret_cast<const f32x4*>(obuf(h) + f);
   }
   if (tid < hmax) {
     const int h = tid;
@@ -765,11 +760,14 @@ __global__ __launch_bounds__(128) void decode_stage2(const float* __restrict__ l
   const int b = blockIdx.x / H, h = blockIdx.x % H;
   const int nq = min(max(num_kv_splits[b] - 1, 1), S1 - 1);
   const int64_t row = ((int64_t)b * H + h) * S1;
+  // unrolled so that the loads of several splits are in flight together
   float M = -3.0e38f;
+#pragma unroll 8
   for (int s = 0; s <= nq; ++s) M = fmaxf(M, lse[row + s]);
   float acc[FPT], den = 0.f;
 #pragma unroll
   for (int i = 0; i < FPT; ++i) acc[i] = 0.f;
+#pragma unroll 8
   for (int s = 0; s <= nq; ++s) {
     const float w = __builtin_amdgcn_exp2f((lse[row + s] - M) * kLog2e);
     den += w;
