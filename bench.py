@@ -50,6 +50,8 @@ def parse():
     ap.add_argument("--splits", type=int, default=0, help="num_kv_splits per request (0 = pick the fastest)")
     ap.add_argument("--no-writer", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--copy-probe", action="store_true",
+                    help="only time a 1 GiB device copy (the reference kernel for rocprofv3 byte counters)")
     return ap.parse_args()
 
 
@@ -122,11 +124,21 @@ class DecodeBench:
                                self.kv_indices, self.seq_lens, self.req, self.ns, self.max_splits,
                                self.logits, self.lse, self.out, self.sm_scale, self.P, self.W, self.PAGE)
 
-    def bytes_per_layer(self) -> float:
+    def step_partials(self):
+        """Stage 1 alone (the dominant kernel), one launch per layer."""
+        from mla_kv_quant_amd import kernels
+
+        for c in self.caches:
+            kernels.decode_partials(c["q"], c["codes"], c["params"], c["rope"], c["hp"], self.kv_indptr,
+                                    self.kv_indices, self.seq_lens, self.req, self.ns, self.max_splits,
+                                    self.logits, self.lse, self.sm_scale, self.P, self.W, self.PAGE)
+
+    def bytes_per_layer(self, with_out: bool = True) -> float:
+        """Algorithmic bytes: 288 B per INT2 token, window rows, q (and the bf16 output)."""
         B, L, P, W, D, R, H = self.B, self.L, self.P, self.W, self.D, self.R, self.H
         int2 = B * (L - P - W) * (D // 4 + 8 * (D // 128) + 2 * R)
         window = B * (P + W) * (2 * D + 2 * R)
-        q_out = B * H * (D + R) * 2 + B * H * D * 2
+        q_out = B * H * (D + R) * 2 + (B * H * D * 2 if with_out else 0)
         return float(int2 + window + q_out)
 
     def flops_per_layer(self) -> float:
@@ -237,10 +249,20 @@ def read_traffic():
     f = ROOT / "profiles" / "decode_cfg2_traffic.json"
     if f.exists():
         try:
-            return json.loads(f.read_text()).get("hbm_bytes_per_layer")
+            return json.loads(f.read_text()).get("hbm_bytes_per_launch")
         except Exception:
             return None
     return None
+
+
+def copy_probe(nbytes: int = 1 << 30, reps: int = 10) -> float:
+    """Achievable HBM rate: GB/s (read + write) of a device-to-device copy of ``nbytes``."""
+    src = torch.empty(nbytes // 4, dtype=torch.float32, device="cuda").fill_(1.0)
+    dst = torch.empty_like(src)
+    ms = time_loop(lambda: dst.copy_(src), reps, 2)
+    del src, dst
+    torch.cuda.empty_cache()
+    return 2.0 * nbytes / (ms * 1e-3) / 1e9
 
 
 def main():
@@ -254,6 +276,9 @@ def main():
         sys.exit(2)
     dev = "cuda:0"
     torch.cuda.set_device(0)
+    if args.copy_probe:
+        print(json.dumps({"copy_gbs": round(copy_probe(), 1), "bytes": 1 << 30}), flush=True)
+        return
     from mla_kv_quant_amd import _lib
 
     _lib.load()
@@ -275,8 +300,14 @@ def main():
     ms = time_loop(db.step, args.steps, args.warmup)
     us_layer = ms * 1000.0 / args.layers
     bpl = db.bytes_per_layer()
-    achieved = bpl / (us_layer * 1e-6) / 1e9
-    print(f"[bench] decode: {us_layer:.2f} us/layer, {achieved:.0f} GB/s", file=sys.stderr, flush=True)
+    # the dominant kernel (stage 1) timed alone: same events, same stream, one launch per layer
+    ms1 = time_loop(db.step_partials, args.steps, args.warmup)
+    us_stage1 = ms1 * 1000.0 / args.layers
+    b1 = db.bytes_per_layer(with_out=False)
+    achieved = b1 / (us_stage1 * 1e-6) / 1e9
+    copy_gbs = copy_probe()
+    print(f"[bench] decode: {us_layer:.2f} us/layer; stage 1 {us_stage1:.2f} us/launch, {achieved:.0f} GB/s "
+          f"(device copy {copy_gbs:.0f} GB/s)", file=sys.stderr, flush=True)
 
     result = {
         "metric": "INT2 MLA decode attn us/layer (cfg2: B=32 x 16K, H=16, D=512, R=64)",
@@ -297,8 +328,12 @@ def main():
                    "num_kv_splits": best[0]},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": read_traffic(),
-                     "algorithmic_bytes_per_layer": bpl,
-                     "mfma_frac": round(db.flops_per_layer() / (us_layer * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4)},
+                     "kernel": "decode_stage1<512,64,paged>", "us_per_launch": round(us_stage1, 3),
+                     "algorithmic_bytes_per_launch": b1,
+                     "layer_frac": round(bpl / (us_layer * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+                     "copy_gbs": round(copy_gbs, 1),
+                     "frac_of_copy": round(achieved / copy_gbs, 4),
+                     "mfma_frac": round(db.flops_per_layer() / (us_stage1 * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4)},
     }
     if not args.no_writer:
         del db.caches

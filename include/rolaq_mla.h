@@ -119,6 +119,31 @@ int rolaq_decode_fwd(const void* q, int64_t q_stride_b, int64_t q_stride_h, cons
                      int P, int W, float sm_scale, float* attn_logits, float* attn_lse,
                      void* out, int64_t out_stride_b, int64_t out_stride_h, void* stream);
 
+/*
+ * Stage 1 of rolaq_decode_fwd alone: the split partials and their LSE, with
+ * the same arguments and rules (no output). Replaces the quantized stage-1
+ * grid plus _fwd_hp_window_stage1 of packed_mla_decode_gf_fwd
+ * (deployment/patches/rolaq_sglang.patch:94-111), for callers that merge
+ * themselves or time the stages apart.
+ */
+int rolaq_decode_partials(const void* q, int64_t q_stride_b, int64_t q_stride_h, const uint8_t* codes,
+                          const float* params, const void* rope_buf, const void* hp_c,
+                          const int32_t* kv_indptr, const int32_t* kv_indices, int page_size,
+                          const int64_t* seq_lens, const int64_t* req_idx,
+                          const int32_t* num_kv_splits, int max_kv_splits, int B, int H, int D,
+                          int R, int P, int W, float sm_scale, float* attn_logits, float* attn_lse,
+                          void* stream);
+
+/*
+ * Stage 2 of rolaq_decode_fwd alone: out[b, h] = sum_s exp(lse_s - LSE) *
+ * attn_logits[b, h, s] over the max(ns_b - 1, 1) + 1 partials of request b,
+ * as bf16. Replaces the softmax-reduce stage that merges ns_merge splits
+ * (ns_merge = quant + 1, deployment/patches/rolaq_sglang.patch:81-92).
+ */
+int rolaq_decode_merge(const float* attn_logits, const float* attn_lse, const int32_t* num_kv_splits,
+                       int max_kv_splits, int B, int H, int D, void* out, int64_t out_stride_b,
+                       int64_t out_stride_h, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -147,6 +147,64 @@ int rolaq_prepare_gf_splits(const int32_t* splits, int32_t* quant, int32_t* merg
                     "prepare_gf_splits launch");
 }
 
+}  // extern "C"
+
+namespace {
+
+// Validates the stage-1 arguments shared by decode_fwd and decode_partials and
+// fills the kernel argument block.
+int decode_args(const char* who, const void* q, int64_t q_stride_b, int64_t q_stride_h, const uint8_t* codes,
+                const float* params, const void* rope_buf, const void* hp_c, const int32_t* kv_indptr,
+                const int32_t* kv_indices, int page_size, const int64_t* seq_lens, const int64_t* req_idx,
+                const int32_t* num_kv_splits, int max_kv_splits, int B, int H, int D, int R, int P, int W,
+                float sm_scale, float* attn_logits, float* attn_lse, rolaq::DecodeArgs* a) {
+  if (!((D == 512 && R == 64) || (D == 256 && R == 32)))
+    return fail(ROLAQ_ERR_INVALID, "%s: (D, R) must be (512, 64) or (256, 32), got (%d, %d)", who, D, R);
+  if (H <= 0 || H > kMaxHeads) return fail(ROLAQ_ERR_INVALID, "%s: head count %d outside 1..%d", who, H, kMaxHeads);
+  if (!q || !codes || !params || !rope_buf || !hp_c || !kv_indptr || !kv_indices || !req_idx || !num_kv_splits ||
+      !attn_logits || !attn_lse)
+    return fail(ROLAQ_ERR_INVALID, "%s: null pointer", who);
+  if (page_size < 1 || (page_size & (page_size - 1)))
+    return fail(ROLAQ_ERR_INVALID, "%s: page_size must be a power of two, got %d", who, page_size);
+  if (!seq_lens && page_size != 1) return fail(ROLAQ_ERR_INVALID, "%s: seq_lens required when page_size > 1", who);
+  if (max_kv_splits < 1 || max_kv_splits > 4096) return fail(ROLAQ_ERR_INVALID, "%s: max_kv_splits out of range", who);
+  if (P < 0 || W < 0 || P + W > 32) return fail(ROLAQ_ERR_INVALID, "%s: need 0 <= P, W and P + W <= 32", who);
+  if (!aligned(q, 16) || q_stride_b % 8 || q_stride_h % 8 || q_stride_h < D + R)
+    return fail(ROLAQ_ERR_INVALID, "%s: q must be 16-byte aligned with strides multiple of 8 and q_stride_h >= D+R", who);
+  if (!aligned(codes, 16) || !aligned(params, 16) || !aligned(rope_buf, 16) || !aligned(hp_c, 16))
+    return fail(ROLAQ_ERR_INVALID, "%s: cache buffers must be 16-byte aligned", who);
+  if (!(sm_scale > 0.f) || !std::isfinite(sm_scale)) return fail(ROLAQ_ERR_INVALID, "%s: invalid sm_scale", who);
+  int shift = 0;
+  while ((1 << shift) < page_size) ++shift;
+  *a = rolaq::DecodeArgs{};
+  a->q = static_cast<const uint16_t*>(q);
+  a->q_sb = q_stride_b;
+  a->q_sh = q_stride_h;
+  a->codes = codes;
+  a->params = params;
+  a->rope = static_cast<const uint16_t*>(rope_buf);
+  a->hp = static_cast<const uint16_t*>(hp_c);
+  a->kv_indptr = kv_indptr;
+  a->kv_indices = kv_indices;
+  a->page_shift = shift;
+  a->seq_lens = seq_lens;
+  a->req_idx = req_idx;
+  a->num_kv_splits = num_kv_splits;
+  a->S1 = max_kv_splits + 1;
+  a->B = B;
+  a->H = H;
+  a->P = P;
+  a->W = W;
+  a->sm_scale = sm_scale;
+  a->logits = attn_logits;
+  a->lse = attn_lse;
+  return ROLAQ_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
 int rolaq_decode_fwd(const void* q, int64_t q_stride_b, int64_t q_stride_h, const uint8_t* codes,
                      const float* params, const void* rope_buf, const void* hp_c, const int32_t* kv_indptr,
                      const int32_t* kv_indices, int page_size, const int64_t* seq_lens, const int64_t* req_idx,
@@ -155,49 +213,55 @@ int rolaq_decode_fwd(const void* q, int64_t q_stride_b, int64_t q_stride_h, cons
                      int64_t out_stride_h, void* stream) {
   if (B < 0) return fail(ROLAQ_ERR_INVALID, "decode_fwd: B < 0");
   if (B == 0) { g_err[0] = '\0'; return ROLAQ_OK; }
-  if (!((D == 512 && R == 64) || (D == 256 && R == 32)))
-    return fail(ROLAQ_ERR_INVALID, "decode_fwd: (D, R) must be (512, 64) or (256, 32), got (%d, %d)", D, R);
-  if (H <= 0 || H > kMaxHeads) return fail(ROLAQ_ERR_INVALID, "decode_fwd: head count %d outside 1..%d", H, kMaxHeads);
-  if (!q || !codes || !params || !rope_buf || !hp_c || !kv_indptr || !kv_indices || !req_idx || !num_kv_splits ||
-      !attn_logits || !attn_lse || !out)
-    return fail(ROLAQ_ERR_INVALID, "decode_fwd: null pointer");
-  if (page_size < 1 || (page_size & (page_size - 1)))
-    return fail(ROLAQ_ERR_INVALID, "decode_fwd: page_size must be a power of two, got %d", page_size);
-  if (!seq_lens && page_size != 1) return fail(ROLAQ_ERR_INVALID, "decode_fwd: seq_lens required when page_size > 1");
-  if (max_kv_splits < 1 || max_kv_splits > 4096) return fail(ROLAQ_ERR_INVALID, "decode_fwd: max_kv_splits out of range");
-  if (P < 0 || W < 0 || P + W > 32) return fail(ROLAQ_ERR_INVALID, "decode_fwd: need 0 <= P, W and P + W <= 32");
-  if (!aligned(q, 16) || q_stride_b % 8 || q_stride_h % 8 || q_stride_h < D + R)
-    return fail(ROLAQ_ERR_INVALID, "decode_fwd: q must be 16-byte aligned with strides multiple of 8 and q_stride_h >= D+R");
-  if (!aligned(codes, 16) || !aligned(params, 16) || !aligned(rope_buf, 16) || !aligned(hp_c, 16))
-    return fail(ROLAQ_ERR_INVALID, "decode_fwd: cache buffers must be 16-byte aligned");
-  if (!(sm_scale > 0.f) || !std::isfinite(sm_scale)) return fail(ROLAQ_ERR_INVALID, "decode_fwd: invalid sm_scale");
-  int shift = 0;
-  while ((1 << shift) < page_size) ++shift;
+  rolaq::DecodeArgs a;
+  const int rc = decode_args("decode_fwd", q, q_stride_b, q_stride_h, codes, params, rope_buf, hp_c, kv_indptr,
+                             kv_indices, page_size, seq_lens, req_idx, num_kv_splits, max_kv_splits, B, H, D, R, P,
+                             W, sm_scale, attn_logits, attn_lse, &a);
+  if (rc != ROLAQ_OK) return rc;
+  if (!out) return fail(ROLAQ_ERR_INVALID, "decode_fwd: null pointer");
+  return hip_status(rolaq_launch_decode(a, D, R, max_kv_splits, static_cast<uint16_t*>(out), out_stride_b,
+                                        out_stride_h, kStagePartials | kStageMerge, static_cast<hipStream_t>(stream)),
+                    "decode_fwd launch");
+}
+
+int rolaq_decode_partials(const void* q, int64_t q_stride_b, int64_t q_stride_h, const uint8_t* codes,
+                          const float* params, const void* rope_buf, const void* hp_c, const int32_t* kv_indptr,
+                          const int32_t* kv_indices, int page_size, const int64_t* seq_lens,
+                          const int64_t* req_idx, const int32_t* num_kv_splits, int max_kv_splits, int B, int H,
+                          int D, int R, int P, int W, float sm_scale, float* attn_logits, float* attn_lse,
+                          void* stream) {
+  if (B < 0) return fail(ROLAQ_ERR_INVALID, "decode_partials: B < 0");
+  if (B == 0) { g_err[0] = '\0'; return ROLAQ_OK; }
+  rolaq::DecodeArgs a;
+  const int rc = decode_args("decode_partials", q, q_stride_b, q_stride_h, codes, params, rope_buf, hp_c, kv_indptr,
+                             kv_indices, page_size, seq_lens, req_idx, num_kv_splits, max_kv_splits, B, H, D, R, P,
+                             W, sm_scale, attn_logits, attn_lse, &a);
+  if (rc != ROLAQ_OK) return rc;
+  return hip_status(rolaq_launch_decode(a, D, R, max_kv_splits, nullptr, 0, 0, kStagePartials,
+                                        static_cast<hipStream_t>(stream)),
+                    "decode_partials launch");
+}
+
+int rolaq_decode_merge(const float* attn_logits, const float* attn_lse, const int32_t* num_kv_splits,
+                       int max_kv_splits, int B, int H, int D, void* out, int64_t out_stride_b,
+                       int64_t out_stride_h, void* stream) {
+  if (B < 0) return fail(ROLAQ_ERR_INVALID, "decode_merge: B < 0");
+  if (B == 0) { g_err[0] = '\0'; return ROLAQ_OK; }
+  if (D != 512 && D != 256) return fail(ROLAQ_ERR_INVALID, "decode_merge: D must be 256 or 512, got %d", D);
+  if (H <= 0 || H > kMaxHeads) return fail(ROLAQ_ERR_INVALID, "decode_merge: head count %d outside 1..%d", H, kMaxHeads);
+  if (max_kv_splits < 1 || max_kv_splits > 4096) return fail(ROLAQ_ERR_INVALID, "decode_merge: max_kv_splits out of range");
+  if (!attn_logits || !attn_lse || !num_kv_splits || !out) return fail(ROLAQ_ERR_INVALID, "decode_merge: null pointer");
+  if (!aligned(attn_logits, 16)) return fail(ROLAQ_ERR_INVALID, "decode_merge: attn_logits must be 16-byte aligned");
   rolaq::DecodeArgs a{};
-  a.q = static_cast<const uint16_t*>(q);
-  a.q_sb = q_stride_b;
-  a.q_sh = q_stride_h;
-  a.codes = codes;
-  a.params = params;
-  a.rope = static_cast<const uint16_t*>(rope_buf);
-  a.hp = static_cast<const uint16_t*>(hp_c);
-  a.kv_indptr = kv_indptr;
-  a.kv_indices = kv_indices;
-  a.page_shift = shift;
-  a.seq_lens = seq_lens;
-  a.req_idx = req_idx;
   a.num_kv_splits = num_kv_splits;
   a.S1 = max_kv_splits + 1;
   a.B = B;
   a.H = H;
-  a.P = P;
-  a.W = W;
-  a.sm_scale = sm_scale;
-  a.logits = attn_logits;
-  a.lse = attn_lse;
-  return hip_status(rolaq_launch_decode(a, D, R, max_kv_splits, static_cast<uint16_t*>(out), out_stride_b,
-                                        out_stride_h, static_cast<hipStream_t>(stream)),
-                    "decode_fwd launch");
+  a.logits = const_cast<float*>(attn_logits);
+  a.lse = const_cast<float*>(attn_lse);
+  return hip_status(rolaq_launch_decode(a, D, D == 512 ? 64 : 32, max_kv_splits, static_cast<uint16_t*>(out),
+                                        out_stride_b, out_stride_h, kStageMerge, static_cast<hipStream_t>(stream)),
+                    "decode_merge launch");
 }
 
 }  // extern "C"

@@ -787,19 +787,23 @@ __global__ __launch_bounds__(128) void decode_stage2(const float* __restrict__ l
 // Host launchers (called from api.cpp).
 // ---------------------------------------------------------------------------
 hipError_t rolaq_launch_decode(const rolaq::DecodeArgs& a, int D, int R, int max_splits,
-                               uint16_t* out, int64_t o_sb, int64_t o_sh, hipStream_t stream) {
+                               uint16_t* out, int64_t o_sb, int64_t o_sh, int stages,
+                               hipStream_t stream) {
   using namespace rolaq;
-  // one block per (sequence, 16 heads, split)
+  // stage 1: one block per (sequence, 16 heads, split); stage 2: one per (sequence, head)
   const dim3 grid(a.B * ((a.H + 15) / 16), max_splits + 1), block(kThreads);
-#define ROLAQ_DEC(DD, RR)                                                              \
-  if (D == DD && R == RR) {                                                            \
-    if (a.page_shift >= 5)                                                             \
-      hipLaunchKernelGGL((decode_stage1<DD, RR, true>), grid, block, 0, stream, a);    \
-    else                                                                               \
-      hipLaunchKernelGGL((decode_stage1<DD, RR, false>), grid, block, 0, stream, a);   \
-    hipLaunchKernelGGL((decode_stage2<DD>), dim3(a.B * a.H), dim3(128), 0, stream,      \
-                       a.logits, a.lse, a.num_kv_splits, a.H, a.S1, out, o_sb, o_sh);  \
-    return hipGetLastError();                                                          \
+#define ROLAQ_DEC(DD, RR)                                                                \
+  if (D == DD && R == RR) {                                                              \
+    if (stages & kStagePartials) {                                                       \
+      if (a.page_shift >= 5)                                                             \
+        hipLaunchKernelGGL((decode_stage1<DD, RR, true>), grid, block, 0, stream, a);    \
+      else                                                                               \
+        hipLaunchKernelGGL((decode_stage1<DD, RR, false>), grid, block, 0, stream, a);   \
+    }                                                                                    \
+    if (stages & kStageMerge)                                                            \
+      hipLaunchKernelGGL((decode_stage2<DD>), dim3(a.B * a.H), dim3(128), 0, stream,      \
+                         a.logits, a.lse, a.num_kv_splits, a.H, a.S1, out, o_sb, o_sh);  \
+    return hipGetLastError();                                                            \
   }
   ROLAQ_DEC(512, 64)
   ROLAQ_DEC(256, 32)

@@ -64,8 +64,10 @@ struct WriterArgs {
 
 // Host launchers (defined next to their kernels).
 #include <hip/hip_runtime.h>
+// stages: kStagePartials (split partials + LSE), kStageMerge (LSE merge -> out), or both
+constexpr int kStagePartials = 1, kStageMerge = 2;
 hipError_t rolaq_launch_decode(const rolaq::DecodeArgs& a, int D, int R, int max_splits, uint16_t* out,
-                               int64_t o_sb, int64_t o_sh, hipStream_t stream);
+                               int64_t o_sb, int64_t o_sh, int stages, hipStream_t stream);
 hipError_t rolaq_launch_pack_f32(const float* x, int64_t xs, const int32_t* slots, int64_t n, int D,
                                  float thr, float kscale, uint8_t* codes, float* params, hipStream_t stream);
 hipError_t rolaq_launch_pack_bf16_aux(const uint16_t* x, int64_t xs, const int64_t* loc, int64_t n, int D,

@@ -123,12 +123,8 @@ def prepare_gf_splits(splits: torch.Tensor, quant: torch.Tensor, merge: torch.Te
                                                    _stream(splits)))
 
 
-def decode_fwd(q: torch.Tensor, codes: torch.Tensor, params: torch.Tensor, rope_buf: torch.Tensor,
-               hp_c: torch.Tensor, kv_indptr: torch.Tensor, kv_indices: torch.Tensor,
-               seq_lens: torch.Tensor | None, req_idx: torch.Tensor, num_kv_splits: torch.Tensor,
-               max_kv_splits: int, attn_logits: torch.Tensor, attn_lse: torch.Tensor,
-               out: torch.Tensor, sm_scale: float, P: int, W: int, page_size: int = 1) -> torch.Tensor:
-    """Absorbed decode over the packed cache: ``q [B, H, D+R]`` -> ``out [B, H, D]``."""
+def _decode_check(q, codes, params, rope_buf, hp_c, kv_indptr, kv_indices, seq_lens, req_idx, num_kv_splits,
+                  max_kv_splits, attn_logits, attn_lse):
     dev = q.device
     _need(q, "q", torch.bfloat16, dev, 3)
     B, H, DR = q.shape
@@ -158,6 +154,11 @@ def decode_fwd(q: torch.Tensor, codes: torch.Tensor, params: torch.Tensor, rope_
         _contig(seq_lens, "seq_lens")
         if seq_lens.numel() < B:
             raise ValueError("seq_lens is shorter than the batch")
+    _scratch_check(attn_logits, attn_lse, B, H, D, max_kv_splits, dev)
+    return B, H, D, R
+
+
+def _scratch_check(attn_logits, attn_lse, B, H, D, max_kv_splits, dev):
     S1 = int(max_kv_splits) + 1
     _need(attn_logits, "attn_logits", torch.float32, dev)
     _need(attn_lse, "attn_lse", torch.float32, dev)
@@ -165,12 +166,58 @@ def decode_fwd(q: torch.Tensor, codes: torch.Tensor, params: torch.Tensor, rope_
     if tuple(attn_logits.shape[1:]) != (H, S1, D) or attn_logits.shape[0] < B \
             or tuple(attn_lse.shape[1:]) != (H, S1) or attn_lse.shape[0] < B:
         raise ValueError("attn_logits / attn_lse must be [>=B, H, max_kv_splits + 1, (D)]")
+
+
+def _out_check(out, B, H, D, dev):
     _need(out, "out", torch.bfloat16, dev, 3)
     if tuple(out.shape) != (B, H, D) or out.stride(2) != 1:
         raise ValueError("out must be [B, H, D] with a contiguous last dim")
+
+
+def decode_fwd(q: torch.Tensor, codes: torch.Tensor, params: torch.Tensor, rope_buf: torch.Tensor,
+               hp_c: torch.Tensor, kv_indptr: torch.Tensor, kv_indices: torch.Tensor,
+               seq_lens: torch.Tensor | None, req_idx: torch.Tensor, num_kv_splits: torch.Tensor,
+               max_kv_splits: int, attn_logits: torch.Tensor, attn_lse: torch.Tensor,
+               out: torch.Tensor, sm_scale: float, P: int, W: int, page_size: int = 1) -> torch.Tensor:
+    """Absorbed decode over the packed cache: ``q [B, H, D+R]`` -> ``out [B, H, D]``."""
+    B, H, D, R = _decode_check(q, codes, params, rope_buf, hp_c, kv_indptr, kv_indices, seq_lens, req_idx,
+                               num_kv_splits, max_kv_splits, attn_logits, attn_lse)
+    _out_check(out, B, H, D, q.device)
     _lib.check(_lib.load().rolaq_decode_fwd(
         _p(q), q.stride(0), q.stride(1), _p(codes), _p(params), _p(rope_buf), _p(hp_c),
         _p(kv_indptr), _p(kv_indices), int(page_size), _p(seq_lens), _p(req_idx), _p(num_kv_splits),
         int(max_kv_splits), B, H, D, R, int(P), int(W), float(sm_scale), _p(attn_logits),
         _p(attn_lse), _p(out), out.stride(0), out.stride(1), _stream(q)))
+    return out
+
+
+def decode_partials(q: torch.Tensor, codes: torch.Tensor, params: torch.Tensor, rope_buf: torch.Tensor,
+                    hp_c: torch.Tensor, kv_indptr: torch.Tensor, kv_indices: torch.Tensor,
+                    seq_lens: torch.Tensor | None, req_idx: torch.Tensor, num_kv_splits: torch.Tensor,
+                    max_kv_splits: int, attn_logits: torch.Tensor, attn_lse: torch.Tensor,
+                    sm_scale: float, P: int, W: int, page_size: int = 1) -> None:
+    """Stage 1 of :func:`decode_fwd` alone: fills ``attn_logits`` / ``attn_lse``."""
+    B, H, D, R = _decode_check(q, codes, params, rope_buf, hp_c, kv_indptr, kv_indices, seq_lens, req_idx,
+                               num_kv_splits, max_kv_splits, attn_logits, attn_lse)
+    _lib.check(_lib.load().rolaq_decode_partials(
+        _p(q), q.stride(0), q.stride(1), _p(codes), _p(params), _p(rope_buf), _p(hp_c),
+        _p(kv_indptr), _p(kv_indices), int(page_size), _p(seq_lens), _p(req_idx), _p(num_kv_splits),
+        int(max_kv_splits), B, H, D, R, int(P), int(W), float(sm_scale), _p(attn_logits),
+        _p(attn_lse), _stream(q)))
+
+
+def decode_merge(attn_logits: torch.Tensor, attn_lse: torch.Tensor, num_kv_splits: torch.Tensor,
+                 max_kv_splits: int, out: torch.Tensor) -> torch.Tensor:
+    """Stage 2 of :func:`decode_fwd` alone: LSE merge of the partials into ``out [B, H, D]``."""
+    dev = out.device
+    _need(num_kv_splits, "num_kv_splits", torch.int32, dev, 1)
+    _contig(num_kv_splits, "num_kv_splits")
+    B, H, D = out.shape
+    if num_kv_splits.numel() < B:
+        raise ValueError("num_kv_splits is shorter than the batch")
+    _scratch_check(attn_logits, attn_lse, B, H, D, max_kv_splits, dev)
+    _out_check(out, B, H, D, dev)
+    _lib.check(_lib.load().rolaq_decode_merge(
+        _p(attn_logits), _p(attn_lse), _p(num_kv_splits), int(max_kv_splits), B, H, D, _p(out),
+        out.stride(0), out.stride(1), _stream(out)))
     return out

@@ -19,7 +19,7 @@ def declared_symbols():
 def test_header_declares_the_entry_points():
     syms = declared_symbols()
     for name in ("rolaq_last_error", "rolaq_abi_version", "rolaq_scatter_pack_rows", "rolaq_write_rows",
-                 "rolaq_prepare_gf_splits", "rolaq_decode_fwd"):
+                 "rolaq_prepare_gf_splits", "rolaq_decode_fwd", "rolaq_decode_partials", "rolaq_decode_merge"):
         assert name in syms
 
 
@@ -55,6 +55,16 @@ def test_invalid_arguments_are_rejected_before_any_launch():
     args[9] = 1
     args[15] = 129  # more heads than the grid supports
     assert lib.rolaq_decode_fwd(*args) == _lib.ROLAQ_ERR_INVALID
+    # stage 1 alone takes the same arguments minus the output
+    pargs = args[:21] + [p, p, None]
+    args[15] = 16
+    pargs[9] = 3
+    assert lib.rolaq_decode_partials(*pargs) == _lib.ROLAQ_ERR_INVALID
+    assert b"decode_partials" in lib.rolaq_last_error()
+    # stage 2 alone: D must be a cache width, pointers non-null
+    assert lib.rolaq_decode_merge(p, p, p, 8, 4, 16, 384, p, 8192, 512, None) == _lib.ROLAQ_ERR_INVALID
+    assert lib.rolaq_decode_merge(None, p, p, 8, 4, 16, 512, p, 8192, 512, None) == _lib.ROLAQ_ERR_INVALID
+    assert lib.rolaq_decode_merge(None, None, None, 8, 0, 16, 512, None, 0, 0, None) == _lib.ROLAQ_OK
 
 
 def test_check_raises_value_error():

@@ -134,3 +134,32 @@ def test_packed_mla_decode_entry_and_prepare_splits():
     torch.testing.assert_close(o.double().cpu(), ref, rtol=RTOL, atol=ATOL)
     with pytest.raises(ValueError):
         packed_mla_decode_gf_fwd(q, o, pool, 0, indptr, indices, ns, 8, logits, lse, sm)  # no req indices
+
+
+def test_partials_then_merge_equals_fused_call():
+    """Stage 1 and stage 2 called apart give the fused call's bytes exactly."""
+    D, R, H, P, W = 512, 64, 16, 4, 16
+    lengths = [5, 300, 1500]
+    pool, slots, pages, reqs, _ = build_pool(lengths, D, R, P, W, 64, seed=31)
+    gp = pool_to_gpu(pool)
+    sm = 1 / math.sqrt(192)
+    q = make_queries(len(lengths), H, D, R, sm, seed=9).to(DEV)
+    splits = [2, 5, 9]
+    out, logits, lse = run_decode(gp, q, slots, pages, lengths, reqs, 64, splits, 12, P, W, sm)
+    indptr, indices = index_lists(slots, pages, 64)
+    seq = torch.tensor(lengths, dtype=torch.int64, device=DEV)
+    req = torch.tensor(reqs, dtype=torch.int64, device=DEV)
+    ns = torch.tensor(splits, dtype=torch.int32, device=DEV)
+    B = len(lengths)
+    l2 = torch.full((B, H, 13, D), float("nan"), device=DEV)
+    s2 = torch.full((B, H, 13), float("nan"), device=DEV)
+    o2 = torch.empty(B, H, D, dtype=torch.bfloat16, device=DEV)
+    kernels.decode_partials(q, gp["codes"], gp["params"], gp["rope"], gp["hp"], indptr, indices, seq, req, ns, 12,
+                            l2, s2, sm, P, W, 64)
+    kernels.decode_merge(l2, s2, ns, 12, o2)
+    torch.cuda.synchronize()
+    for b, n in enumerate(splits):
+        k = max(n - 1, 1) + 1
+        assert torch.equal(l2[b, :, :k].cpu(), logits[b, :, :k])
+        assert torch.equal(s2[b, :, :k].cpu(), lse[b, :, :k])
+    assert torch.equal(o2.float().cpu(), out)
