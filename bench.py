@@ -50,6 +50,7 @@ def parse():
     ap.add_argument("--splits", type=int, default=0, help="num_kv_splits per request (0 = pick the fastest)")
     ap.add_argument("--no-writer", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--writer-only", action="store_true", help="only the cfg1 writer (prints its own JSON)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only time a 1 GiB device copy (the reference kernel for rocprofv3 byte counters)")
     return ap.parse_args()
@@ -265,6 +266,25 @@ def copy_probe(nbytes: int = 1 << 30, reps: int = 10) -> float:
     return 2.0 * nbytes / (ms * 1e-3) / 1e9
 
 
+def writer_result(args, dev: str) -> dict:
+    wb = WriterBench(args.layers, dev)
+    wms = time_loop(wb.step, max(3, args.steps // 2), args.warmup)
+    wus = wms * 1000.0 / args.layers
+    wach = wb.bytes_per_layer() / (wus * 1e-6) / 1e9
+    res = {
+        "workload": "cfg1 writer: 64 seqs x 2048-token prefill chunk, 27 layers with own buffers",
+        "mtokens_per_s": round(wb.n * args.layers / (wms * 1e-3) / 1e6, 1),
+        "us_per_layer": round(wus, 3),
+        "hbm_achieved_gbs": round(wach, 1),
+        "hbm_frac": round(wach / HBM_PEAK_GBS, 4),
+        "mfma_frac": round(wb.flops_per_layer() / (wus * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
+    }
+    print(f"[bench] writer: {wus:.2f} us/layer, {res['mtokens_per_s']} Mtok/s", file=sys.stderr, flush=True)
+    del wb
+    torch.cuda.empty_cache()
+    return res
+
+
 def main():
     args = parse()
     if args.gpus != 1:
@@ -282,6 +302,9 @@ def main():
     from mla_kv_quant_amd import _lib
 
     _lib.load()
+    if args.writer_only:
+        print(json.dumps(writer_result(args, dev)), flush=True)
+        return
     t_setup = time.time()
     db = DecodeBench(args.layers, dev)
     print(f"[bench] decode caches written for {args.layers} layers in {time.time() - t_setup:.1f}s", file=sys.stderr,
@@ -338,22 +361,7 @@ def main():
     if not args.no_writer:
         del db.caches
         torch.cuda.empty_cache()
-        wb = WriterBench(args.layers, dev)
-        wms = time_loop(wb.step, max(3, args.steps // 2), args.warmup)
-        wus = wms * 1000.0 / args.layers
-        wach = wb.bytes_per_layer() / (wus * 1e-6) / 1e9
-        result["writer"] = {
-            "workload": "cfg1 writer: 64 seqs x 2048-token prefill chunk, 27 layers with own buffers",
-            "mtokens_per_s": round(wb.n * args.layers / (wms * 1e-3) / 1e6, 1),
-            "us_per_layer": round(wus, 3),
-            "hbm_achieved_gbs": round(wach, 1),
-            "hbm_frac": round(wach / HBM_PEAK_GBS, 4),
-            "mfma_frac": round(wb.flops_per_layer() / (wus * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
-        }
-        print(f"[bench] writer: {wus:.2f} us/layer, {result['writer']['mtokens_per_s']} Mtok/s", file=sys.stderr,
-              flush=True)
-        del wb
-        torch.cuda.empty_cache()
+        result["writer"] = writer_result(args, dev)
         if not args.no_cpu:
             db = DecodeBench(1, dev)
     if not args.no_cpu:

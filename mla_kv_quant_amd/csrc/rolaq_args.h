@@ -58,6 +58,7 @@ struct WriterArgs {
   int32_t* row_of_slot;
   int32_t* owner_of_row;
   int nstripes;
+  int pe_vec;  // k_pe rows copied as dword pairs (set by the launcher)
 };
 
 }  // namespace rolaq

@@ -10,28 +10,67 @@
 // products as the reference's FP32 GEMM; only the summation order differs.
 //
 // Decomposition: a block owns one quantization group g (128 output columns)
-// and keeps that slice of R_eff^T in LDS for its lifetime; its 4 waves each
-// take 64-row tiles of a stripe of rows. Blocks of the NG groups of one stripe
-// are numbered so that they land on the same XCD and read the same latent rows
-// through one L2. Per tile a wave computes C^T[col, row] with MFMA 16x16x32
-// (M = 16 columns, N = 16 rows, K = 32), so each lane ends up with 32 values of
-// one row: row statistics need a 4-lane reduction and the codes of a packed
-// word come from 4 lanes.
+// and keeps that slice of R_eff^T in LDS for its lifetime; its 8 waves (two per
+// SIMD, so one wave's epilogue overlaps the other's MFMAs) each take 64-row
+// tiles of a stripe of rows. Per tile a wave computes C^T[col, row] with MFMA
+// 16x16x32 (M = 16 columns, N = 16 rows, K = 32) from LDS (R) and latent rows
+// loaded straight into registers a few K-steps ahead; the LDS rows are
+// permuted so that each lane ends up with whole packed words of one row.
 #include "rolaq_common.h"
 #include "rolaq_args.h"
 
 namespace rolaq {
 
+constexpr int kWriterWaves = 8;   // waves per block: two per SIMD, so one's epilogue overlaps the other's MFMAs
+constexpr int kWriterRows = 64;   // latent rows per wave tile
+constexpr int kWriterDepth = 2;   // K-steps of latent loads in flight per wave (divides D / 32)
+constexpr int kBufferFlags = 0x00020000;  // buffer descriptor word 3 for gfx9 raw buffers
+
+// Column (within group g) held by row m of the block's LDS copy of R_g^T.
+// Output block mb of a tile gives lane (la, gq) the rows 4 gq + i (i = 0..3)
+// of that block; mapping them to columns 32 gq + 16 (mb / 4) + 4 (mb % 4) + i
+// hands every lane two whole packed words (words 2 gq, 2 gq + 1 of the group)
+// and 32 consecutive columns, so packing and stores need no lane exchange.
+__host__ __device__ constexpr int writer_col(int m) {
+  return 32 * ((m & 15) >> 2) + 16 * ((m >> 4) >> 2) + 4 * ((m >> 4) & 3) + (m & 3);
+}
+
+// Sum over the lanes l, l ^ 16, l ^ 32, l ^ 48 (same la, all gq) with the
+// gfx950 row-swap permutes: VALU only, no LDS round trip.
+__device__ __forceinline__ float sum_over_rows(float v) {
+  const auto h = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  v = __uint_as_float(h[0]) + __uint_as_float(h[1]);
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// floor(x) as int32 in one instruction (v_cvt_flr_i32_f32; saturates, which
+// the caller's clamp to 0..3 absorbs).
+__device__ __forceinline__ int floor_to_int(float x) {
+  int r;
+  asm("v_cvt_flr_i32_f32 %0, %1" : "=v"(r) : "v"(x));
+  return r;
+}
 
 template <int D>
-__global__ __launch_bounds__(256, 1) void writer_kernel(WriterArgs a) {
-  constexpr int NG = D / 128;
-  constexpr int KS = D / 32;              // K-steps
-  constexpr int LDS_STRIDE = 2 * D + 16;  // bytes per LDS column (padded)
-  constexpr int WROWS = 64;               // rows per wave tile
+struct WriterGeo {
+  static constexpr int NG = D / 128;
+  static constexpr int KS = D / 32;            // MFMA K-steps
+  static constexpr int STRIDE = 2 * D + 16;    // bytes per LDS row (padded)
+  static constexpr int LDS_BYTES = 128 * STRIDE;
+};
+
+// Block = one quantization group g x a stripe of 64-row tiles. The block's
+// R_g^T slice stays in LDS; its eight waves each own whole tiles and never
+// synchronise after staging. Blocks of the NG groups of one stripe get the same
+// blockIdx % 8, i.e. the same XCD, so each latent row is fetched from HBM once
+// and served to the other groups from that XCD's L2.
+template <int D>
+__global__ __launch_bounds__(64 * kWriterWaves, 1) void writer_kernel(WriterArgs a) {
+  using G = WriterGeo<D>;
+  constexpr int NG = G::NG, KS = G::KS, STR = G::STRIDE;
   extern __shared__ __attribute__((aligned(16))) uint8_t s_rt[];
 
-  // block -> (group, stripe); blocks of one stripe share w % 8 (same XCD)
   const int w = blockIdx.x;
   int g, stripe;
   if (a.nstripes % 8 == 0) {
@@ -41,142 +80,183 @@ __global__ __launch_bounds__(256, 1) void writer_kernel(WriterArgs a) {
     g = w % NG;
     stripe = w / NG;
   }
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int gq = lane >> 4, la = lane & 15;
 
-  // ---- stage R_eff^T rows [128g, 128g + 128) into LDS ------------------------
+  // ---- stage the permuted rows of R_eff^T for group g ------------------------
   {
-    const uint8_t* src = reinterpret_cast<const uint8_t*>(a.rt + (int64_t)(128 * g) * D);
-    constexpr int CHUNKS = 128 * D * 2 / 16;
-    for (int c = tid; c < CHUNKS; c += 256) {
-      const int col = c / (D * 2 / 16), off = (c % (D * 2 / 16)) * 16;
-      *reinterpret_cast<u32x4*>(s_rt + col * LDS_STRIDE + off) =
-          *reinterpret_cast<const u32x4*>(src + (int64_t)col * D * 2 + off);
+    constexpr int CPR = 2 * D / 16;  // 16-byte chunks per row
+    const uint8_t* src = reinterpret_cast<const uint8_t*>(a.rt);
+#pragma unroll 8
+    for (int c = tid; c < 128 * CPR; c += 64 * kWriterWaves) {
+      const int m = c / CPR, off = (c % CPR) * 16;
+      const int64_t col = 128 * g + writer_col(m);
+      *reinterpret_cast<u32x4*>(s_rt + m * STR + off) =
+          *reinterpret_cast<const u32x4*>(src + col * (2 * D) + off);
     }
   }
   __syncthreads();
 
-  const int64_t nrb = (a.n + 4 * WROWS - 1) / (4 * WROWS);
-  for (int64_t rb = stripe; rb < nrb; rb += a.nstripes) {
-    const int64_t row0 = rb * 4 * WROWS + wave * WROWS;
-    if (row0 >= a.n) continue;
+  const float inv_t = 1.0f / a.thr;
+  const int64_t ntiles = (a.n + kWriterRows - 1) / kWriterRows;
+  const int64_t tstep = (int64_t)a.nstripes * kWriterWaves;
+  const uint8_t* lds_a = s_rt + la * STR + 16 * gq;
+
+  // Latent rows go into registers kWriterDepth K-steps ahead; the ring runs
+  // on across tiles, so the next tile's first steps are in flight while this
+  // tile's epilogue runs. The loads are coalesced -- lanes 4r..4r+3 read the
+  // 64 contiguous bytes of row r for one K-step -- and each K-step's data is
+  // moved to the MFMA lane layout (lane la + 16 gq <- lane 4 la + gq) with
+  // ds_bpermute. (Loading the MFMA layout directly makes every 16-lane pass of
+  // a load touch 16 rows, which leaves the texture path four times busier.)
+  // They are buffer loads over the tile's rows: one per-lane offset for the
+  // whole kernel, the row block and K-step in the scalar and immediate
+  // offsets, rows at or past n read as zeros.
+  const int xrow = (int)a.xs * 2;                          // bytes per latent row
+  const int voff = (lane >> 2) * xrow + 16 * (lane & 3);
+  const int perm = 4 * (4 * la + gq);                      // ds_bpermute source address
+  auto tile_rsrc = [&](int64_t t0) {
+    const int64_t rows = min((int64_t)kWriterRows, a.n - t0 * kWriterRows);
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<uint16_t*>(a.x) + t0 * kWriterRows * a.xs, (short)0,
+                                             (int)(rows > 0 ? rows * xrow : 0), kBufferFlags);
+  };
+  auto xload = [&](__amdgpu_buffer_rsrc_t rs, int nb, int k) {
+    return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, voff + 64 * k, nb * 16 * xrow, 0));
+  };
+  auto relayout = [&](u32x4 v) {
+    return u32x4{(uint32_t)__builtin_amdgcn_ds_bpermute(perm, (int)v.x),
+                 (uint32_t)__builtin_amdgcn_ds_bpermute(perm, (int)v.y),
+                 (uint32_t)__builtin_amdgcn_ds_bpermute(perm, (int)v.z),
+                 (uint32_t)__builtin_amdgcn_ds_bpermute(perm, (int)v.w)};
+  };
+  u32x4 xb[kWriterDepth][4];
+  int64_t t = (int64_t)stripe * kWriterWaves + wave;
+  {
+    const __amdgpu_buffer_rsrc_t rs = tile_rsrc(t);
+#pragma unroll
+    for (int d = 0; d < kWriterDepth; ++d)
+#pragma unroll
+      for (int nb = 0; nb < 4; ++nb) xb[d][nb] = xload(rs, nb, d);
+  }
+  // low dwords of the int64 row metadata (sequence lengths, positions and
+  // request indices fit in 32 bits; -1 stays -1)
+  const int32_t* seq32 = reinterpret_cast<const int32_t*>(a.seq_lens);
+  // decode rows (no positions) sit at seq_len - 1: read seq_lens there instead
+  const int32_t* pos32 = reinterpret_cast<const int32_t*>(a.positions ? a.positions : a.seq_lens);
+  const int32_t pos_adj = a.positions ? 0 : -1;
+  const int32_t* req32 = reinterpret_cast<const int32_t*>(a.req_idx);
+
+  for (; t < ntiles; t += tstep) {
+    const int64_t row0 = t * kWriterRows;
+    const __amdgpu_buffer_rsrc_t rs = tile_rsrc(t), rn = tile_rsrc(t + tstep);
+
+    // ---- C^T tile: 128 columns x 64 rows on MFMA 16x16x32 ----------------------
     f32x4 acc[8][4];
 #pragma unroll
     for (int mb = 0; mb < 8; ++mb)
 #pragma unroll
       for (int nb = 0; nb < 4; ++nb) acc[mb][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
-    const uint16_t* xr[4];
 #pragma unroll
-    for (int nb = 0; nb < 4; ++nb) {
-      const int64_t r = min(row0 + 16 * nb + la, a.n - 1);
-      xr[nb] = a.x + r * a.xs + 8 * gq;
-    }
-    u32x4 bcur[4], bnext[4];
-#pragma unroll
-    for (int nb = 0; nb < 4; ++nb) bcur[nb] = *reinterpret_cast<const u32x4*>(xr[nb]);
-#pragma unroll 2
     for (int ks = 0; ks < KS; ++ks) {
-      if (ks + 1 < KS) {
+      const int cur = ks % kWriterDepth;
+      u32x4 av[8], xv[4];
 #pragma unroll
-        for (int nb = 0; nb < 4; ++nb) bnext[nb] = *reinterpret_cast<const u32x4*>(xr[nb] + 32 * (ks + 1));
-      }
+      for (int mb = 0; mb < 8; ++mb) av[mb] = *reinterpret_cast<const u32x4*>(lds_a + 16 * mb * STR + 64 * ks);
 #pragma unroll
-      for (int mb = 0; mb < 8; ++mb) {
-        const u32x4 av = *reinterpret_cast<const u32x4*>(s_rt + (16 * mb + la) * LDS_STRIDE + (32 * ks + 8 * gq) * 2);
+      for (int nb = 0; nb < 4; ++nb) xv[nb] = relayout(xb[cur][nb]);
+      const int kk = ks + kWriterDepth;
 #pragma unroll
-        for (int nb = 0; nb < 4; ++nb) acc[mb][nb] = mfma16x16x32(av, bcur[nb], acc[mb][nb]);
-      }
-      if (ks + 1 < KS) {
-#pragma unroll
-        for (int nb = 0; nb < 4; ++nb) bcur[nb] = bnext[nb];
-      }
-    }
-
-    // ---- epilogue: one row per lane per N-block ------------------------------
-#pragma unroll
-    for (int nb = 0; nb < 4; ++nb) {
-      const int64_t row = row0 + 16 * nb + la;
-      const bool live = row < a.n;
-      // acc[mb][nb][j]: column 16mb + 4gq + j of group g for this row
-      float s = 0.f;
+      for (int nb = 0; nb < 4; ++nb) xb[cur][nb] = kk < KS ? xload(rs, nb, kk) : xload(rn, nb, kk - KS);
 #pragma unroll
       for (int mb = 0; mb < 8; ++mb)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) s += acc[mb][nb][j];
-      s = wave_sum_over_groups(s);
+        for (int nb = 0; nb < 4; ++nb) acc[mb][nb] = mfma16x16x32(av[mb], xv[nb], acc[mb][nb]);
+      // one K-step per scheduling region: hoisting every step's LDS reads
+      // ahead of the unrolled loop would exhaust the registers
+      __builtin_amdgcn_sched_barrier(0);
+    }
+
+    // ---- epilogue: lane (la, gq) holds columns 32gq..32gq+31 of row 16nb+la ---
+    int64_t slot[4];
+    int32_t seq[4], pos[4], req[4];
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb) {
+      const int64_t r = min(row0 + 16 * nb + la, a.n - 1);
+      slot[nb] = a.loc[r];
+      seq[nb] = seq32[2 * r];
+      pos[nb] = pos32[2 * r] + pos_adj;
+      req[nb] = req32[2 * r];
+    }
+#pragma unroll
+    for (int nb = 0; nb < 4; ++nb) {
+      __builtin_amdgcn_sched_barrier(0);
+      const int64_t row = row0 + 16 * nb + la;
+      // rope columns [16 g, 16 g + 16) of the row, four per lane
+      u32x2 pe = {0u, 0u};
+      if (a.pe_vec) pe = *reinterpret_cast<const u32x2*>(a.k_pe + min(row, a.n - 1) * a.pe_s0 + 16 * g + 4 * gq);
+      const bool live = row < a.n;
+      const int64_t sl = slot[nb];
+      // window bookkeeping (mla_fused_writer.py:36-51)
+      const int32_t p = pos[nb], sq = seq[nb], rq = req[nb];
+      const bool keep = live && ((p < a.P) || (p >= sq - a.W)) && rq < a.max_reqs && rq >= 0 && sl > 0;
+      const int32_t inner = p < a.P ? p : a.P + (p - a.P > 0 ? p - a.P : 0) % (a.W > 0 ? a.W : 1);
+      const int64_t ring = 1 + (int64_t)rq * (a.P + a.W) + inner;
+      if (keep) {
+        // bf16 of the rotated FP32 row (columns 32gq..32gq+31 of group g)
+        uint16_t* hrow = a.hp + ring * D + 128 * g + 32 * gq;
+#pragma unroll
+        for (int h = 0; h < 4; ++h) {
+          const f32x4 u = acc[2 * h][nb], v = acc[2 * h + 1][nb];
+          const u32x4 pk = {pack_bf16(u[0], u[1]), pack_bf16(u[2], u[3]), pack_bf16(v[0], v[1]),
+                            pack_bf16(v[2], v[3])};
+          *reinterpret_cast<u32x4*>(hrow + 8 * h) = pk;
+        }
+      }
+      // Lloyd statistics over the row's 128 group columns (4 lanes)
+      float s = 0.f;
+#pragma unroll
+      for (int mb = 0; mb < 8; ++mb) s += (acc[mb][nb][0] + acc[mb][nb][1]) + (acc[mb][nb][2] + acc[mb][nb][3]);
+      s = sum_over_rows(s);
       const float mean = s * (1.0f / 128.0f);
       float q = 0.f;
 #pragma unroll
       for (int mb = 0; mb < 8; ++mb)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const float d = acc[mb][nb][j] - mean;
-          q = fmaf(d, d, q);
+        for (int i = 0; i < 4; ++i) {
+          acc[mb][nb][i] -= mean;
+          q = fmaf(acc[mb][nb][i], acc[mb][nb][i], q);
         }
-      q = wave_sum_over_groups(q);
+      q = sum_over_rows(q);
       const float std_ = sqrtf(q * (1.0f / 128.0f) + 1e-08f);
-      const float inv = 1.0f / std_;
-      // byte gq of word mb: codes of columns 16mb + 4gq + j at bits 2j
-      uint32_t lo = 0, hi = 0;
+      // code = #{-t, 0, t <= (x - mean) / std} = clamp(floor((x - mean) / (t std) + 2), 0, 3)
+      const float k = (1.0f / std_) * inv_t;
+      uint32_t word[2] = {0u, 0u};
 #pragma unroll
-      for (int mb = 0; mb < 8; ++mb) {
-        uint32_t byte = 0;
+      for (int mb = 0; mb < 8; ++mb)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const float nrm = (acc[mb][nb][j] - mean) * inv;
-          const uint32_t c = uint32_t(nrm >= -a.thr) + uint32_t(nrm >= 0.f) + uint32_t(nrm >= a.thr);
-          byte |= c << (2 * j);
+        for (int i = 0; i < 4; ++i) {
+          const int c = min(max(floor_to_int(fmaf(acc[mb][nb][i], k, 2.0f)), 0), 3);
+          word[mb >> 2] |= uint32_t(c) << (2 * (4 * (mb & 3) + i));
         }
-        if (mb < 4) lo |= byte << (8 * mb); else hi |= byte << (8 * (mb - 4));
-      }
-      // lane gq assembles words 2gq, 2gq+1 from the four lanes of this row
-      const uint32_t mine = gq < 2 ? lo : hi;  // dword holding words 2gq, 2gq+1 bytes
-      uint32_t src[4];
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        const uint32_t lo_k = __shfl(lo, la + 16 * k);
-        const uint32_t hi_k = __shfl(hi, la + 16 * k);
-        src[k] = gq < 2 ? lo_k : hi_k;
-      }
-      (void)mine;
-      const int bsel0 = (2 * gq) % 4, bsel1 = (2 * gq + 1) % 4;
-      uint32_t w0 = 0, w1 = 0;
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        w0 |= ((src[k] >> (8 * bsel0)) & 0xffu) << (8 * k);
-        w1 |= ((src[k] >> (8 * bsel1)) & 0xffu) << (8 * k);
-      }
-      const int64_t slot = live ? a.loc[row] : 0;
       if (live) {
-        uint8_t* crow = a.codes + slot * (D / 4);
-        *reinterpret_cast<uint32_t*>(crow + 4 * (NG * (2 * gq) + g)) = w0;
-        *reinterpret_cast<uint32_t*>(crow + 4 * (NG * (2 * gq + 1) + g)) = w1;
+        uint32_t* crow = reinterpret_cast<uint32_t*>(a.codes + sl * (D / 4));
+        crow[NG * (2 * gq) + g] = word[0];
+        crow[NG * (2 * gq + 1) + g] = word[1];
         if (gq == 0) {
           const float scale = a.kscale * std_;
           const float zero = kZeroOffset - mean / scale;
-          *reinterpret_cast<f32x2*>(a.params + slot * 2 * NG + 2 * g) = f32x2{scale, zero};
+          *reinterpret_cast<f32x2*>(a.params + sl * 2 * NG + 2 * g) = f32x2{scale, zero};
         }
-        // window bookkeeping (mla_fused_writer.py:36-51)
-        const int64_t seq = a.seq_lens[row];
-        const int64_t pos = a.positions ? a.positions[row] : seq - 1;
-        const int64_t req = a.req_idx[row];
-        const bool keep = ((pos < a.P) || (pos >= seq - a.W)) && req < a.max_reqs && req >= 0 && slot > 0;
-        const int64_t inner = pos < a.P ? pos : a.P + (pos - a.P > 0 ? pos - a.P : 0) % (a.W > 0 ? a.W : 1);
-        const int64_t ring = 1 + req * (a.P + a.W) + inner;
-        if (keep) {
-          uint16_t* hrow = a.hp + ring * D + 128 * g;
-#pragma unroll
-          for (int mb = 0; mb < 8; ++mb) {
-            const u32x2 v = {pack_bf16(acc[mb][nb][0], acc[mb][nb][1]), pack_bf16(acc[mb][nb][2], acc[mb][nb][3])};
-            *reinterpret_cast<u32x2*>(hrow + 16 * mb + 4 * gq) = v;
+        if (sl > 0) {
+          if (a.pe_vec) {
+            *reinterpret_cast<u32x2*>(a.rope + sl * a.R + 16 * g + 4 * gq) = pe;
+          } else if (g == 0) {
+            for (int r = gq; r < a.R; r += 4) a.rope[sl * a.R + r] = a.k_pe[row * a.pe_s0 + r * a.pe_s1];
           }
-        }
-        if (g == 0 && slot > 0) {
-          for (int r = gq; r < a.R; r += 4)
-            a.rope[slot * a.R + r] = a.k_pe[row * a.pe_s0 + r * a.pe_s1];
-          if (gq == 0) {
-            a.row_of_slot[slot] = keep ? int32_t(ring) : -1;
-            if (keep) a.owner_of_row[ring] = int32_t(slot);
+          if (g == 0 && gq == 0) {
+            a.row_of_slot[sl] = keep ? int32_t(ring) : -1;
+            if (keep) a.owner_of_row[ring] = int32_t(sl);
           }
         }
       }
@@ -190,25 +270,29 @@ hipError_t rolaq_launch_writer(const rolaq::WriterArgs& args_in, int D, int num_
   using namespace rolaq;
   WriterArgs a = args_in;
   const int NG = D / 128;
-  const int64_t nrb = (a.n + 255) / 256;
-  // enough stripes to give every CU one block, in multiples of 8 when large
+  const int64_t ntiles = (a.n + kWriterRows - 1) / kWriterRows;
+  const int64_t need = (ntiles + kWriterWaves - 1) / kWriterWaves;  // stripes with work for every wave
+  // one block per CU (the R_g slice fills most of the LDS), in multiples of 8 when large
   int64_t stripes = (num_cus + NG - 1) / NG;
   if (stripes >= 8) stripes = (stripes / 8) * 8;
-  if (stripes > nrb) stripes = nrb;
+  if (stripes > need) stripes = need;
   if (stripes < 1) stripes = 1;
   a.nstripes = (int)stripes;
-  const dim3 grid((unsigned)(stripes * NG)), block(256);
-  const size_t lds = (size_t)128 * (2 * D + 16);
-  if (D == 512) {
-    const hipError_t e = hipFuncSetAttribute((const void*)writer_kernel<512>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((writer_kernel<512>), grid, block, lds, stream, a);
-  } else if (D == 256) {
-    const hipError_t e = hipFuncSetAttribute((const void*)writer_kernel<256>, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (e != hipSuccess) return e;
-    hipLaunchKernelGGL((writer_kernel<256>), grid, block, lds, stream, a);
-  } else {
-    return hipErrorInvalidValue;
+  // rope copy as 8-byte pieces: 16 columns per group, 8-byte aligned rows
+  a.pe_vec = a.pe_s1 == 1 && a.R == 16 * NG && (a.pe_s0 % 4) == 0 &&
+             (reinterpret_cast<uintptr_t>(a.k_pe) % 8) == 0 && (reinterpret_cast<uintptr_t>(a.rope) % 8) == 0;
+  const dim3 grid((unsigned)(stripes * NG)), block(64 * kWriterWaves);
+#define ROLAQ_WRITER(DD)                                                                               \
+  if (D == DD) {                                                                                      \
+    const int lds = WriterGeo<DD>::LDS_BYTES;                                                         \
+    const hipError_t e =                                                                              \
+        hipFuncSetAttribute((const void*)writer_kernel<DD>, hipFuncAttributeMaxDynamicSharedMemorySize, lds); \
+    if (e != hipSuccess) return e;                                                                    \
+    hipLaunchKernelGGL((writer_kernel<DD>), grid, block, lds, stream, a);                             \
+    return hipGetLastError();                                                                         \
   }
-  return hipGetLastError();
+  ROLAQ_WRITER(512)
+  ROLAQ_WRITER(256)
+#undef ROLAQ_WRITER
+  return hipErrorInvalidValue;
 }
