@@ -144,6 +144,32 @@ int rolaq_decode_merge(const float* attn_logits, const float* attn_lse, const in
                        int max_kv_splits, int B, int H, int D, void* out, int64_t out_stride_b,
                        int64_t out_stride_h, void* stream);
 
+/*
+ * Absorbed MLA extend (chunked prefill) attention over the packed cache.
+ * Replaces: the packed pool's extend reader behind the MLA attention call of
+ *   the patched forward_absorb (deployment/patches/rolaq_sglang.patch:208-235;
+ *   kernel in the un-vendored fork), with the HF cache's row semantics
+ *   (mla_quant/cache.py:1030-1039).
+ * Sequence b has chunk tokens qo_indptr[b] .. qo_indptr[b+1]-1 at positions
+ * prefix_lens[b] + j, over its prefix (slots from kv_indptr/kv_indices, pages
+ * of page_size) and the chunk itself, causally. Prefix position t is read as
+ * the BF16 window row (hp_c ring row of req_idx[b]) when t < P or
+ * t >= prefix_lens[b] + chunk length - W, else dequantized from the INT2 row
+ * ((code - zero) * scale, rounded to bf16). Chunk rows are k_chunk: bf16
+ * [T, D + R] (latent | rope), row stride kc_stride_t.
+ * q: bf16 [T, H, D + R] (q_lat | q_rope), strides (q_stride_t, q_stride_h).
+ * out: bf16 [T, H, D], strides (out_stride_t, out_stride_h), rotated frame.
+ * max_q_len >= every chunk length (sizes the grid). (D, R) = (256, 32) or
+ * (512, 64).
+ */
+int rolaq_extend_fwd(const void* q, int64_t q_stride_t, int64_t q_stride_h, const void* k_chunk,
+                     int64_t kc_stride_t, const int32_t* qo_indptr, const int32_t* kv_indptr,
+                     const int32_t* kv_indices, int page_size, const int64_t* prefix_lens,
+                     const int64_t* req_idx, const uint8_t* codes, const float* params,
+                     const void* rope_buf, const void* hp_c, int B, int H, int D, int R, int P, int W,
+                     int max_q_len, float sm_scale, void* out, int64_t out_stride_t,
+                     int64_t out_stride_h, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -8,6 +8,8 @@ Hand-written HIP kernels for gfx950 behind a C ABI (``include/rolaq_mla.h``,
   rope / BF16-window stores;
 * ``decode.prepare_gf_splits`` / ``decode.packed_mla_decode_gf_fwd`` -- absorbed
   MLA decode over the packed cache with split-K and LSE merge;
+* ``extend.packed_mla_extend_fwd`` -- causal chunked-prefill attention over the
+  packed prefix plus the chunk;
 * ``artifacts`` -- RoLaQ artifact loading and read-rotation folding.
 
 The library is loaded lazily on first use and there is no CPU fallback.

@@ -264,4 +264,58 @@ int rolaq_decode_merge(const float* attn_logits, const float* attn_lse, const in
                     "decode_merge launch");
 }
 
+int rolaq_extend_fwd(const void* q, int64_t q_stride_t, int64_t q_stride_h, const void* k_chunk,
+                     int64_t kc_stride_t, const int32_t* qo_indptr, const int32_t* kv_indptr,
+                     const int32_t* kv_indices, int page_size, const int64_t* prefix_lens,
+                     const int64_t* req_idx, const uint8_t* codes, const float* params, const void* rope_buf,
+                     const void* hp_c, int B, int H, int D, int R, int P, int W, int max_q_len, float sm_scale,
+                     void* out, int64_t out_stride_t, int64_t out_stride_h, void* stream) {
+  if (B < 0 || max_q_len < 0) return fail(ROLAQ_ERR_INVALID, "extend_fwd: B < 0 or max_q_len < 0");
+  if (B == 0 || max_q_len == 0) { g_err[0] = '\0'; return ROLAQ_OK; }
+  if (!((D == 256 && R == 32) || (D == 512 && R == 64)))
+    return fail(ROLAQ_ERR_INVALID, "extend_fwd: (D, R) must be (256, 32) or (512, 64), got (%d, %d)", D, R);
+  if (H <= 0 || H > 4096) return fail(ROLAQ_ERR_INVALID, "extend_fwd: head count %d out of range", H);
+  if (!q || !k_chunk || !qo_indptr || !kv_indptr || !kv_indices || !prefix_lens || !req_idx || !codes || !params ||
+      !rope_buf || !hp_c || !out)
+    return fail(ROLAQ_ERR_INVALID, "extend_fwd: null pointer");
+  if (page_size < 1 || (page_size & (page_size - 1)))
+    return fail(ROLAQ_ERR_INVALID, "extend_fwd: page_size must be a power of two, got %d", page_size);
+  if (P < 0 || W < 0) return fail(ROLAQ_ERR_INVALID, "extend_fwd: negative window");
+  if (!aligned(q, 16) || q_stride_t % 8 || q_stride_h % 8 || q_stride_h < D + R)
+    return fail(ROLAQ_ERR_INVALID, "extend_fwd: q must be 16-byte aligned with strides multiple of 8 and q_stride_h >= D+R");
+  if (!aligned(k_chunk, 16) || kc_stride_t % 8 || kc_stride_t < D + R)
+    return fail(ROLAQ_ERR_INVALID, "extend_fwd: k_chunk must be 16-byte aligned with a row stride >= D+R, multiple of 8");
+  if (!aligned(codes, 16) || !aligned(params, 16) || !aligned(rope_buf, 16) || !aligned(hp_c, 16))
+    return fail(ROLAQ_ERR_INVALID, "extend_fwd: cache buffers must be 16-byte aligned");
+  if (!(sm_scale > 0.f) || !std::isfinite(sm_scale)) return fail(ROLAQ_ERR_INVALID, "extend_fwd: invalid sm_scale");
+  int shift = 0;
+  while ((1 << shift) < page_size) ++shift;
+  rolaq::ExtendArgs a{};
+  a.q = static_cast<const uint16_t*>(q);
+  a.q_st = q_stride_t;
+  a.q_sh = q_stride_h;
+  a.kc = static_cast<const uint16_t*>(k_chunk);
+  a.kc_st = kc_stride_t;
+  a.qo_indptr = qo_indptr;
+  a.kv_indptr = kv_indptr;
+  a.kv_indices = kv_indices;
+  a.page_shift = shift;
+  a.prefix_lens = prefix_lens;
+  a.req_idx = req_idx;
+  a.codes = codes;
+  a.params = params;
+  a.rope = static_cast<const uint16_t*>(rope_buf);
+  a.hp = static_cast<const uint16_t*>(hp_c);
+  a.B = B;
+  a.H = H;
+  a.P = P;
+  a.W = W;
+  a.sm_scale = sm_scale;
+  a.out = static_cast<uint16_t*>(out);
+  a.o_st = out_stride_t;
+  a.o_sh = out_stride_h;
+  return hip_status(rolaq_launch_extend(a, D, R, max_q_len, static_cast<hipStream_t>(stream)), "extend_fwd launch");
+}
+
 }  // extern "C"
+

@@ -61,6 +61,27 @@ struct WriterArgs {
   int pe_vec;  // k_pe rows copied as dword pairs (set by the launcher)
 };
 
+struct ExtendArgs {
+  const uint16_t* q;        // [T, H, D + R] bf16, strides (q_st, q_sh)
+  int64_t q_st, q_sh;
+  const uint16_t* kc;       // chunk keys [T, D + R] bf16, row stride kc_st
+  int64_t kc_st;
+  const int32_t* qo_indptr;  // [B + 1] chunk token offsets
+  const int32_t* kv_indptr;  // prefix page (or token) lists
+  const int32_t* kv_indices;
+  int page_shift;
+  const int64_t* prefix_lens;
+  const int64_t* req_idx;
+  const uint8_t* codes;
+  const float* params;
+  const uint16_t* rope;
+  const uint16_t* hp;
+  int B, H, P, W;
+  float sm_scale;
+  uint16_t* out;            // [T, H, D] bf16, strides (o_st, o_sh)
+  int64_t o_st, o_sh;
+};
+
 }  // namespace rolaq
 
 // Host launchers (defined next to their kernels).
@@ -77,3 +98,4 @@ hipError_t rolaq_launch_pack_bf16_aux(const uint16_t* x, int64_t xs, const int64
 hipError_t rolaq_launch_prepare_splits(const int32_t* splits, int32_t* quant, int32_t* merge, int64_t n,
                                        hipStream_t stream);
 hipError_t rolaq_launch_writer(const rolaq::WriterArgs& a, int D, int num_cus, hipStream_t stream);
+hipError_t rolaq_launch_extend(const rolaq::ExtendArgs& a, int D, int R, int max_q_len, hipStream_t stream);

@@ -221,3 +221,45 @@ def decode_merge(attn_logits: torch.Tensor, attn_lse: torch.Tensor, num_kv_split
         _p(attn_logits), _p(attn_lse), _p(num_kv_splits), int(max_kv_splits), B, H, D, _p(out),
         out.stride(0), out.stride(1), _stream(out)))
     return out
+
+
+def extend_fwd(q: torch.Tensor, k_chunk: torch.Tensor, qo_indptr: torch.Tensor, kv_indptr: torch.Tensor,
+               kv_indices: torch.Tensor, prefix_lens: torch.Tensor, req_idx: torch.Tensor, codes: torch.Tensor,
+               params: torch.Tensor, rope_buf: torch.Tensor, hp_c: torch.Tensor, max_q_len: int,
+               out: torch.Tensor, sm_scale: float, P: int, W: int, page_size: int = 1) -> torch.Tensor:
+    """Causal extend over the packed prefix + the chunk: ``q [T, H, D+R]`` -> ``out [T, H, D]``."""
+    dev = q.device
+    _need(q, "q", torch.bfloat16, dev, 3)
+    T, H, DR = q.shape
+    D = codes.shape[1] * 4
+    R = DR - D
+    if q.stride(2) != 1:
+        raise ValueError("q must be contiguous in its last dim")
+    _need(k_chunk, "k_chunk", torch.bfloat16, dev, 2)
+    if k_chunk.shape[0] < T or k_chunk.shape[1] != DR or k_chunk.stride(1) != 1:
+        raise ValueError("k_chunk must be [T, D + R] with a contiguous last dim")
+    _need(codes, "codes", torch.uint8, dev, 2)
+    _need(params, "params", torch.float32, dev, 3)
+    _need(rope_buf, "rope_buf", torch.bfloat16, dev, 2)
+    _need(hp_c, "hp_c", torch.bfloat16, dev, 2)
+    for name, t in (("codes", codes), ("params", params), ("rope_buf", rope_buf), ("hp_c", hp_c)):
+        _contig(t, name)
+    if rope_buf.shape[1] != R or hp_c.shape[1] != D or tuple(params.shape[1:]) != (D // GROUP_SIZE, 2):
+        raise ValueError("cache buffers do not match q's (D, R)")
+    for name, t, dt in (("qo_indptr", qo_indptr, torch.int32), ("kv_indptr", kv_indptr, torch.int32),
+                        ("kv_indices", kv_indices, torch.int32), ("prefix_lens", prefix_lens, torch.int64),
+                        ("req_idx", req_idx, torch.int64)):
+        _need(t, name, dt, dev, 1)
+        _contig(t, name)
+    B = qo_indptr.numel() - 1
+    if B < 0 or kv_indptr.numel() < B + 1 or prefix_lens.numel() < B or req_idx.numel() < B:
+        raise ValueError("index tensors are shorter than the batch")
+    _need(out, "out", torch.bfloat16, dev, 3)
+    if out.shape[0] < T or tuple(out.shape[1:]) != (H, D) or out.stride(2) != 1:
+        raise ValueError("out must be [T, H, D] with a contiguous last dim")
+    _lib.check(_lib.load().rolaq_extend_fwd(
+        _p(q), q.stride(0), q.stride(1), _p(k_chunk), k_chunk.stride(0), _p(qo_indptr), _p(kv_indptr),
+        _p(kv_indices), int(page_size), _p(prefix_lens), _p(req_idx), _p(codes), _p(params), _p(rope_buf),
+        _p(hp_c), B, H, D, R, int(P), int(W), int(max_q_len), float(sm_scale), _p(out), out.stride(0),
+        out.stride(1), _stream(q)))
+    return out

@@ -19,7 +19,7 @@ def declared_symbols():
 def test_header_declares_the_entry_points():
     syms = declared_symbols()
     for name in ("rolaq_last_error", "rolaq_abi_version", "rolaq_scatter_pack_rows", "rolaq_write_rows",
-                 "rolaq_prepare_gf_splits", "rolaq_decode_fwd", "rolaq_decode_partials", "rolaq_decode_merge"):
+                 "rolaq_prepare_gf_splits", "rolaq_decode_fwd", "rolaq_decode_partials", "rolaq_decode_merge", "rolaq_extend_fwd"):
         assert name in syms
 
 
@@ -65,6 +65,21 @@ def test_invalid_arguments_are_rejected_before_any_launch():
     assert lib.rolaq_decode_merge(p, p, p, 8, 4, 16, 384, p, 8192, 512, None) == _lib.ROLAQ_ERR_INVALID
     assert lib.rolaq_decode_merge(None, p, p, 8, 4, 16, 512, p, 8192, 512, None) == _lib.ROLAQ_ERR_INVALID
     assert lib.rolaq_decode_merge(None, None, None, 8, 0, 16, 512, None, 0, 0, None) == _lib.ROLAQ_OK
+    # extend: shape and pointer checks, empty batch is a no-op
+    eargs = [p, 40 * 288, 288, p, 288, p, p, p, 16, p, p, p, p, p, p, 4, 40, 256, 32, 4, 16, 2048, 0.1, p,
+             40 * 256, 256, None]
+    bad = list(eargs)
+    bad[17], bad[18] = 384, 32
+    assert lib.rolaq_extend_fwd(*bad) == _lib.ROLAQ_ERR_INVALID and b"(D, R)" in lib.rolaq_last_error()
+    bad = list(eargs)
+    bad[8] = 12
+    assert lib.rolaq_extend_fwd(*bad) == _lib.ROLAQ_ERR_INVALID and b"power of two" in lib.rolaq_last_error()
+    bad = list(eargs)
+    bad[3] = None
+    assert lib.rolaq_extend_fwd(*bad) == _lib.ROLAQ_ERR_INVALID
+    bad = list(eargs)
+    bad[15] = 0
+    assert lib.rolaq_extend_fwd(*bad) == _lib.ROLAQ_OK
 
 
 def test_check_raises_value_error():
