@@ -51,6 +51,8 @@ def parse():
     ap.add_argument("--no-writer", action="store_true")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--writer-only", action="store_true", help="only the cfg1 writer (prints its own JSON)")
+    ap.add_argument("--extend-only", action="store_true", help="only the cfg4b extend (prints its own JSON)")
+    ap.add_argument("--no-extend", action="store_true")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only time a 1 GiB device copy (the reference kernel for rocprofv3 byte counters)")
     return ap.parse_args()
@@ -215,6 +217,95 @@ class WriterBench:
 
 
 # ---------------------------------------------------------------------------
+# config 4b: extend (chunked prefill) over the packed prefix
+# ---------------------------------------------------------------------------
+class ExtendBench:
+    B, TQ, PREFIX, H, D, R, P, W, PAGE = 4, 2048, 14336, 40, 256, 32, 4, 16, 64
+
+    def __init__(self, layers: int, dev: str):
+        from mla_kv_quant_amd import kernels, synth
+
+        B, TQ, PF, H, D, R, P, W, PAGE = self.B, self.TQ, self.PREFIX, self.H, self.D, self.R, self.P, self.W, \
+            self.PAGE
+        self.dev = dev
+        pages_per_seq = (PF + TQ) // PAGE
+        perm = np.random.default_rng(2).permutation(np.arange(1, B * pages_per_seq + 1)).astype(np.int64)
+        table = perm.reshape(B, pages_per_seq)
+        num_slots = (B * pages_per_seq + 1) * PAGE
+        # the prefix's pages (the chunk's own rows come from k_chunk)
+        pp = PF // PAGE
+        self.kv_indptr = torch.arange(0, B * pp + 1, pp, dtype=torch.int32, device=dev)
+        self.kv_indices = torch.from_numpy(table[:, :pp].reshape(-1).astype(np.int32)).to(dev)
+        self.qo_indptr = torch.arange(0, B * TQ + 1, TQ, dtype=torch.int32, device=dev)
+        self.prefix = torch.full((B,), PF, dtype=torch.int64, device=dev)
+        self.req = torch.arange(1, B + 1, dtype=torch.int64, device=dev)
+        slots = (torch.from_numpy(table[:, :pp]).to(dev)[:, :, None] * PAGE
+                 + torch.arange(PAGE, device=dev)).reshape(-1).contiguous()
+        positions = torch.arange(PF, device=dev).repeat(B)
+        seqs = torch.full((B * PF,), PF + TQ, dtype=torch.int64, device=dev)
+        reqs = self.req.repeat_interleave(PF)
+        max_reqs = B + 1
+        hp_rows = 1 + max_reqs * (P + W)
+        self.sm_scale = 1.0 / math.sqrt(96)
+        sigma = 2.0 / (self.sm_scale * math.sqrt(D + R))
+        self.layers = []
+        for layer in range(layers):
+            c = {
+                "codes": torch.zeros(num_slots, D // 4, dtype=torch.uint8, device=dev),
+                "params": torch.zeros(num_slots, D // 128, 2, dtype=torch.float32, device=dev),
+                "rope": torch.zeros(num_slots, R, dtype=torch.bfloat16, device=dev),
+                "hp": torch.zeros(hp_rows, D, dtype=torch.bfloat16, device=dev),
+                "row": torch.full((num_slots,), -1, dtype=torch.int32, device=dev),
+                "owner": torch.zeros(hp_rows, dtype=torch.int32, device=dev),
+            }
+            rt = synth.layer_rotation(D, layer).to(torch.bfloat16).t().contiguous().to(dev)
+            x = synth.make_latent(B * PF, D, max(1, D // 100), seed=60_000 + layer, device=dev)
+            pe = synth.make_normal((B * PF, R), 61_000 + layer, device=dev)
+            kernels.write_rows(x, pe, rt, slots, seqs, positions, reqs, c["codes"], c["params"], c["rope"],
+                               c["hp"], c["row"], c["owner"], P, W, max_reqs, synth.DEFAULT_THRESHOLD,
+                               synth.DEFAULT_GAIN)
+            del x, pe
+            c["q"] = synth.make_normal((B * TQ, H, D + R), 62_000 + layer, std=sigma, device=dev)
+            c["kc"] = torch.cat([synth.make_latent(B * TQ, D, 3, seed=63_000 + layer, device=dev),
+                                 synth.make_normal((B * TQ, R), 64_000 + layer, device=dev)], 1).contiguous()
+            self.layers.append(c)
+        self.out = torch.empty(B * TQ, H, D, dtype=torch.bfloat16, device=dev)
+        torch.cuda.synchronize()
+
+    def step(self):
+        from mla_kv_quant_amd import kernels
+
+        for c in self.layers:
+            kernels.extend_fwd(c["q"], c["kc"], self.qo_indptr, self.kv_indptr, self.kv_indices, self.prefix,
+                               self.req, c["codes"], c["params"], c["rope"], c["hp"], self.TQ, self.out,
+                               self.sm_scale, self.P, self.W, self.PAGE)
+
+    def flops_per_layer(self) -> float:
+        """Algorithmic flops: 2 H (2 D + R) per (query, visible key) pair."""
+        B, TQ, PF, H, D, R = self.B, self.TQ, self.PREFIX, self.H, self.D, self.R
+        pairs = B * (TQ * PF + TQ * (TQ + 1) // 2)
+        return float(2 * H * (2 * D + R) * pairs)
+
+
+def extend_result(args, dev: str, layers: int = 2) -> dict:
+    eb = ExtendBench(layers, dev)
+    ms = time_loop(eb.step, max(2, args.steps // 4), 1)
+    ms_layer = ms / layers
+    tflops = eb.flops_per_layer() / (ms_layer * 1e-3) / 1e12
+    res = {
+        "workload": "cfg4b extend: batch 4 x 2048 causal queries over a 14336-token INT2 prefix + s4r16 window, "
+                    "40 heads, latent 256, rope 32, page 64",
+        "ms_per_layer": round(ms_layer, 4),
+        "tflops": round(tflops, 1),
+        "mfma_frac": round(tflops / MFMA_BF16_PEAK_TFLOPS, 4),
+    }
+    print(f"[bench] extend: {ms_layer:.3f} ms/layer, {tflops:.0f} TFLOP/s", file=sys.stderr, flush=True)
+    del eb
+    torch.cuda.empty_cache()
+    return res
+
+
+# ---------------------------------------------------------------------------
 # CPU baseline (oracle on the host cores)
 # ---------------------------------------------------------------------------
 def cpu_baseline(db: DecodeBench, seqs: int = 2):
@@ -305,6 +396,9 @@ def main():
     if args.writer_only:
         print(json.dumps(writer_result(args, dev)), flush=True)
         return
+    if args.extend_only:
+        print(json.dumps(extend_result(args, dev)), flush=True)
+        return
     t_setup = time.time()
     db = DecodeBench(args.layers, dev)
     print(f"[bench] decode caches written for {args.layers} layers in {time.time() - t_setup:.1f}s", file=sys.stderr,
@@ -358,13 +452,16 @@ def main():
                      "frac_of_copy": round(achieved / copy_gbs, 4),
                      "mfma_frac": round(db.flops_per_layer() / (us_stage1 * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4)},
     }
-    if not args.no_writer:
+    if not args.no_writer or not args.no_extend:
         del db.caches
         torch.cuda.empty_cache()
+    if not args.no_writer:
         result["writer"] = writer_result(args, dev)
-        if not args.no_cpu:
-            db = DecodeBench(1, dev)
+    if not args.no_extend:
+        result["extend"] = extend_result(args, dev)
     if not args.no_cpu:
+        if not hasattr(db, "caches"):
+            db = DecodeBench(1, dev)
         result["cpu_baseline"] = cpu_baseline(db)
     print(json.dumps(result), flush=True)
 

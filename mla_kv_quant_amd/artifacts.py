@@ -1,10 +1,22 @@
-"""RoLaQ artifact loader and read-rotation folding (host side).
+"""RoLaQ artifact loading and read-rotation folding (host side).
 
-Restates deployment/sglang/srt/mem_cache/rolaq_mla.py:16-71 (manifest checks,
-per-layer ``(threshold, gain)``, ``W_b @ fp32(bf16(R))``) with the rotation
-checks of mla_quant/quantizer.py:145-152. An artifact is a directory holding
-``manifest.json`` and ``layer_<i>.pt`` (FP32 ``[D, D]`` rotations), loaded with
-``torch.load(..., weights_only=True)``.
+An artifact is a directory with ``manifest.json`` and one FP32 rotation per
+decoder layer (``layer_<i>.pt``), in the format the reference writes
+(mla_quant/quantizer.py:155-215). The drop-in entry points keep the
+reference's names, arguments and ``ValueError`` behaviour:
+
+* ``load_layer_quantizers(path, rotation_path, group_size, width, layer_ids)``
+  -> per-layer ``(threshold, gain)`` or ``None`` without an artifact
+  (deployment/sglang/srt/mem_cache/rolaq_mla.py:41-53);
+* ``fold_read_rotation(weight, layer_id, rotation_path)`` -> ``bf16(W_b @
+  fp32(bf16(R)))`` (rolaq_mla.py:56-71).
+
+``Artifact`` gathers the checks the reference spreads over its loaders
+(rolaq_mla.py:16-38, quantizer.py:145-152 and 217-252, deployment/serve.py:20-56):
+manifest schema, every layer present, SHA-256 of every rotation file, finite
+positive quantizer parameters, and -- when a rotation is read -- square, FP32,
+finite and orthogonal to 1e-5. Rotations are read with
+``torch.load(..., weights_only=True)`` only.
 """
 
 from __future__ import annotations
@@ -12,6 +24,7 @@ from __future__ import annotations
 import hashlib
 import json
 import math
+from dataclasses import dataclass
 from functools import lru_cache
 from pathlib import Path
 
@@ -19,90 +32,127 @@ import torch
 
 RECIPE = "learned_shared_latent_rotation_quantizer_v2"
 FORMAT_VERSION = 2
+GROUP_SIZE = 128
+
+# manifest field -> the value a packed-INT2 (oscar_lloyd, content-only) artifact must hold
+_REQUIRED = (
+    ("recipe", RECIPE, "not a frozen v2 learned RoLaQ artifact"),
+    ("family", "oscar_lloyd", "only the oscar_lloyd quantizer family is supported by the packed writer"),
+    ("components", ["nope"], "expected a content-only (nope) artifact"),
+    ("group_size", GROUP_SIZE, "expected quantization groups of 128"),
+)
 
 
-def _sha256(path: Path) -> str:
-    h = hashlib.sha256()
-    with path.open("rb") as f:
-        for chunk in iter(lambda: f.read(1 << 20), b""):
-            h.update(chunk)
-    return h.hexdigest()
+def file_sha256(path: Path) -> str:
+    digest = hashlib.sha256()
+    with Path(path).open("rb") as f:
+        for block in iter(lambda: f.read(1 << 20), b""):
+            digest.update(block)
+    return digest.hexdigest()
 
 
-@lru_cache(maxsize=8)
-def load_manifest(path):
-    """Validate and return the manifest (rolaq_mla.py:16-38)."""
-    root = Path(path).resolve()
-    manifest = json.loads((root / "manifest.json").read_text())
-    if manifest.get("recipe") != RECIPE:
-        raise ValueError("RoLaQ requires a frozen v2 learned artifact")
-    if manifest.get("family") != "oscar_lloyd":
-        raise ValueError("The packed RoLaQ writer currently supports oscar_lloyd only")
-    if manifest.get("components") != ["nope"] or manifest.get("group_size") != 128:
-        raise ValueError("Expected content-only, group-128 RoLaQ artifact")
-    count = manifest["model"]["num_hidden_layers"]
-    if set(manifest["layers"]) != {str(i) for i in range(count)}:
-        raise ValueError("RoLaQ artifact must cover every decoder layer")
-    for layer, item in manifest["layers"].items():
-        if item["file"] != f"layer_{int(layer)}.pt":
-            raise ValueError("Unexpected rotation filename")
-        if _sha256(root / item["file"]) != item["sha256"]:
-            raise ValueError(f"RoLaQ rotation hash mismatch: layer {layer}")
-        t, gain = item["param0"], item["param1"]
-        if not (math.isfinite(t) and math.isfinite(gain) and t > 0 and gain > 0):
-            raise ValueError(f"Invalid quantizer parameters at layer {layer}")
-    return manifest
-
-
-def load_layer_quantizers(path, rotation_path, group_size, width, layer_ids):
-    """Per-layer ``(threshold, gain)`` or ``None`` without an artifact (rolaq_mla.py:41-53)."""
-    if not path:
-        return [None for _ in layer_ids]
-    if Path(path).resolve() != Path(rotation_path).resolve():
-        raise ValueError("Learned quantizer and rotations must come from the same artifact")
-    manifest = load_manifest(path)
-    if manifest["group_size"] != group_size or manifest["model"]["kv_lora_rank"] != width:
-        raise ValueError("RoLaQ artifact does not match the cache dimensions")
-    out = []
-    for layer in layer_ids:
-        item = manifest["layers"][str(layer)]
-        out.append((float(item["param0"]), float(item["param1"])))
-    return out
-
-
-def load_rotation(rotation_path, layer_id: int, width: int | None = None) -> torch.Tensor:
-    """FP32 rotation of one layer, checked square/finite/orthogonal (quantizer.py:145-152)."""
-    rotation = torch.load(Path(rotation_path) / f"layer_{layer_id}.pt", map_location="cpu", weights_only=True)
+def check_rotation(rotation, width: int | None, layer) -> torch.Tensor:
+    """Square FP32, finite, ``|R^T R - I|_max <= 1e-5`` (quantizer.py:145-152)."""
     if not isinstance(rotation, torch.Tensor) or rotation.dtype != torch.float32 or rotation.dim() != 2 \
             or rotation.shape[0] != rotation.shape[1] or (width is not None and rotation.shape[0] != width):
-        raise ValueError(f"layer {layer_id} requires a square FP32 rotation")
-    if not torch.isfinite(rotation).all():
-        raise ValueError(f"layer {layer_id} rotation contains non-finite values")
-    n = rotation.shape[0]
-    residual = (rotation.double().T @ rotation.double() - torch.eye(n, dtype=torch.float64)).abs().max().item()
+        raise ValueError(f"layer {layer}: rotation must be a square FP32 matrix of the latent width")
+    if not bool(torch.isfinite(rotation).all()):
+        raise ValueError(f"layer {layer}: rotation has non-finite entries")
+    r = rotation.double()
+    residual = float((r.T @ r - torch.eye(r.shape[0], dtype=torch.float64)).abs().max())
     if residual > 1e-05:
-        raise ValueError(f"layer {layer_id} rotation not orthogonal, residual={residual}")
+        raise ValueError(f"layer {layer}: rotation is not orthogonal (residual {residual:.3g})")
     return rotation
 
 
-def fold_read_rotation(weight, layer_id, rotation_path):
-    """Return ``W_b @ R`` for derived MLA readers (rolaq_mla.py:56-71).
+@dataclass(frozen=True)
+class LayerRecord:
+    file: str
+    sha256: str
+    threshold: float
+    gain: float
 
-    ``W_b`` is ``[heads * (key_dim + value_dim), latent_dim]`` bf16; the product
-    is formed in FP32 with ``R_eff = fp32(bf16(R))`` and rounded to bf16.
+
+class Artifact:
+    """A validated artifact directory (manifest checked on construction)."""
+
+    def __init__(self, path):
+        self.root = Path(path).resolve()
+        manifest = json.loads((self.root / "manifest.json").read_text())
+        for key, want, why in _REQUIRED:
+            if manifest.get(key) != want:
+                raise ValueError(f"RoLaQ artifact: {why}")
+        model = manifest.get("model") or {}
+        count = int(model["num_hidden_layers"])
+        self.width = int(model["kv_lora_rank"])
+        if set(manifest["layers"]) != {str(i) for i in range(count)}:
+            raise ValueError("RoLaQ artifact must hold exactly one record per decoder layer")
+        self.layers: dict[int, LayerRecord] = {}
+        for key, item in manifest["layers"].items():
+            layer = int(key)
+            if item["file"] != f"layer_{layer}.pt":
+                raise ValueError(f"layer {layer}: unexpected rotation file name {item['file']!r}")
+            if file_sha256(self.root / item["file"]) != item["sha256"]:
+                raise ValueError(f"layer {layer}: rotation file does not match its SHA-256")
+            t, g = item["param0"], item["param1"]
+            if not all(isinstance(v, (int, float)) and math.isfinite(v) and v > 0 for v in (t, g)):
+                raise ValueError(f"layer {layer}: quantizer threshold/gain must be finite and positive")
+            self.layers[layer] = LayerRecord(item["file"], item["sha256"], float(t), float(g))
+        self.manifest = manifest
+
+    def quantizer(self, layer: int) -> tuple[float, float]:
+        rec = self.layers[int(layer)]
+        return rec.threshold, rec.gain
+
+    def rotation(self, layer: int, width: int | None = None) -> torch.Tensor:
+        rec = self.layers[int(layer)]
+        r = torch.load(self.root / rec.file, map_location="cpu", weights_only=True)
+        return check_rotation(r, width if width is not None else self.width, layer)
+
+
+@lru_cache(maxsize=8)
+def open_artifact(path) -> Artifact:
+    return Artifact(path)
+
+
+def load_layer_quantizers(path, rotation_path, group_size, width, layer_ids):
+    """Per-layer ``(threshold, gain)``; ``[None] * len(layer_ids)`` without an artifact."""
+    if not path:
+        return [None for _ in layer_ids]
+    if Path(path).resolve() != Path(rotation_path).resolve():
+        raise ValueError("the quantizer parameters and the rotations must come from one artifact")
+    art = open_artifact(str(Path(path).resolve()))
+    if group_size != GROUP_SIZE or art.width != width:
+        raise ValueError("RoLaQ artifact does not match the cache's group size / latent width")
+    return [art.quantizer(layer) for layer in layer_ids]
+
+
+def load_rotation(rotation_path, layer_id: int, width: int | None = None) -> torch.Tensor:
+    """The checked FP32 rotation of one layer (no manifest needed)."""
+    r = torch.load(Path(rotation_path) / f"layer_{layer_id}.pt", map_location="cpu", weights_only=True)
+    return check_rotation(r, width, layer_id)
+
+
+def fold_read_rotation(weight, layer_id, rotation_path):
+    """``bf16(W_b @ fp32(bf16(R)))`` for the absorbed MLA readers.
+
+    ``W_b`` is ``[heads * (key_dim + value_dim), latent_dim]`` bf16. Queries and
+    outputs of the absorbed path then live in the rotated frame, so the readers
+    apply no rotation at run time. The product is formed in FP32 with the same
+    effective rotation the writer uses (R rounded to bf16, read back as FP32).
     """
     if weight.dtype != torch.bfloat16:
-        raise ValueError("Read-rotation absorption is validated for BF16 weights only")
-    rotation = torch.load(Path(rotation_path) / f"layer_{layer_id}.pt", map_location="cpu", weights_only=True)
-    if rotation.shape != (weight.shape[-1], weight.shape[-1]):
-        raise ValueError("Read-rotation shape mismatch")
-    effective = rotation.to(device=weight.device, dtype=weight.dtype).float()
-    return (weight.float() @ effective).to(weight.dtype)
+        raise ValueError("read-rotation folding is defined for bf16 weights only")
+    r = torch.load(Path(rotation_path) / f"layer_{layer_id}.pt", map_location="cpu", weights_only=True)
+    if tuple(r.shape) != (weight.shape[-1], weight.shape[-1]):
+        raise ValueError("read rotation does not match the weight's latent width")
+    effective = r.to(device=weight.device, dtype=torch.bfloat16).float()
+    return (weight.float() @ effective).to(torch.bfloat16)
 
 
 def write_artifact(root, rotations: dict, params: dict, model: dict) -> dict:
-    """Write a manifest + per-layer rotations in the reference's artifact format
-    (mla_quant/quantizer.py:155-215 field names); used to build test artifacts."""
+    """Write an artifact directory in the reference's format (field names of
+    mla_quant/quantizer.py:190-213); used to build test artifacts."""
     root = Path(root)
     root.mkdir(parents=True, exist_ok=False)
     layers = {}
@@ -110,9 +160,9 @@ def write_artifact(root, rotations: dict, params: dict, model: dict) -> dict:
         path = root / f"layer_{layer}.pt"
         torch.save(rotations[layer].detach().cpu().float().contiguous(), path)
         t, g = params[layer]
-        layers[str(layer)] = {"file": path.name, "sha256": _sha256(path), "param0": float(t), "param1": float(g)}
+        layers[str(layer)] = {"file": path.name, "sha256": file_sha256(path), "param0": float(t), "param1": float(g)}
     manifest = {"format_version": FORMAT_VERSION, "recipe": RECIPE, "family": "oscar_lloyd",
-                "group_size": 128, "components": ["nope"], "windows": False, "model": dict(model),
+                "group_size": GROUP_SIZE, "components": ["nope"], "windows": False, "model": dict(model),
                 "layers": layers}
     (root / "manifest.json").write_text(json.dumps(manifest, indent=2))
     return manifest

@@ -87,3 +87,19 @@ def test_check_raises_value_error():
     rc = lib.rolaq_prepare_gf_splits(None, None, None, 4, None)
     with pytest.raises(ValueError):
         _lib.check(rc)
+
+
+def test_pool_memory_accounting_matches_its_buffers():
+    """get_kv_size_bytes charges per-token rows of every layer, the shared row
+    map once, and the fixed BF16 window arena (rolaq_sglang.patch:166-189)."""
+    import torch
+    from mla_kv_quant_amd import PackedMLAPool
+
+    for D, R, layers, reqs in ((512, 64, 3, 5), (256, 32, 2, 9)):
+        pool = PackedMLAPool(300, layers, D, R, reqs, 4, 16, device="cpu")
+        held = sum(t.numel() * t.element_size() for name in ("c_codes", "c_params", "rope_buf", "hp_c")
+                   for t in getattr(pool, name))
+        held += pool.hp_row_of_slot.numel() * 4 + pool.hp_owner_of_row.numel() * 4
+        assert pool.get_kv_size_bytes() == held
+        per_token = layers * (D // 4 + 8 * (D // 128) + 2 * R) + 4
+        assert per_token == (layers * 288 + 4 if D == 512 else layers * 144 + 4)
