@@ -170,6 +170,24 @@ int rolaq_extend_fwd(const void* q, int64_t q_stride_t, int64_t q_stride_h, cons
                      int max_q_len, float sm_scale, void* out, int64_t out_stride_t,
                      int64_t out_stride_h, void* stream);
 
+/*
+ * Cache rows as bf16 [latent | rope] rows (MHA-style prefill over a packed
+ * prefix). Replaces: the fork's _assemble_rows_kernel
+ *   (deployment/patches/rolaq_sglang.patch:5-6) and the un-rotation of the
+ *   latent for kv_b_proj (deployment/sglang/srt/mem_cache/rolaq_mla.py:60-61).
+ * Row i of out (stride out_stride elements) gets slot slots[i]: the BF16
+ * window row if row_of_slot[slot] = r >= 0 and owner_of_row[r] == slot, else
+ * the INT2 row dequantized ((code - zero) * scale, rounded to bf16); with
+ * rotation (R_eff = bf16(R), [D, D] row-major) the latent is multiplied by
+ * R_eff^T in FP32 and rounded to bf16 (rotate_quantize's cast order,
+ * mla_quant/quantizer.py:117-122); without it the rotated frame is returned.
+ * Columns D .. D + R - 1 are the rope row.
+ */
+int rolaq_assemble_rows(const int64_t* slots, int64_t n, const uint8_t* codes, const float* params,
+                        const void* rope_buf, const void* hp_c, const int32_t* row_of_slot,
+                        const int32_t* owner_of_row, const void* rotation, int D, int R, void* out,
+                        int64_t out_stride, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

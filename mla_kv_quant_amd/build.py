@@ -19,7 +19,7 @@ HERE = Path(__file__).resolve().parent
 CSRC = HERE / "csrc"
 ROOT = HERE.parent
 LIB = HERE / "librolaq_mla.so"
-SOURCES = ["api.cpp", "pack.hip", "writer.hip", "decode.hip", "extend.hip"]
+SOURCES = ["api.cpp", "pack.hip", "writer.hip", "decode.hip", "extend.hip", "assemble.hip"]
 ARCH = "gfx950"
 
 

@@ -317,5 +317,37 @@ int rolaq_extend_fwd(const void* q, int64_t q_stride_t, int64_t q_stride_h, cons
   return hip_status(rolaq_launch_extend(a, D, R, max_q_len, static_cast<hipStream_t>(stream)), "extend_fwd launch");
 }
 
+int rolaq_assemble_rows(const int64_t* slots, int64_t n, const uint8_t* codes, const float* params,
+                        const void* rope_buf, const void* hp_c, const int32_t* row_of_slot,
+                        const int32_t* owner_of_row, const void* rotation, int D, int R, void* out,
+                        int64_t out_stride, void* stream) {
+  if (n < 0) return fail(ROLAQ_ERR_INVALID, "assemble_rows: n < 0");
+  if (n == 0) { g_err[0] = '\0'; return ROLAQ_OK; }
+  if (!((D == 512 && R == 64) || (D == 256 && R == 32)))
+    return fail(ROLAQ_ERR_INVALID, "assemble_rows: (D, R) must be (512, 64) or (256, 32), got (%d, %d)", D, R);
+  if (!slots || !codes || !params || !rope_buf || !hp_c || !row_of_slot || !owner_of_row || !out)
+    return fail(ROLAQ_ERR_INVALID, "assemble_rows: null pointer");
+  if (!aligned(codes, 4) || !aligned(params, 8) || !aligned(rope_buf, 16) || !aligned(hp_c, 16) || !aligned(out, 16) ||
+      (rotation && !aligned(rotation, 16)))
+    return fail(ROLAQ_ERR_INVALID, "assemble_rows: misaligned buffers");
+  if (out_stride < D + R || out_stride % 8)
+    return fail(ROLAQ_ERR_INVALID, "assemble_rows: out row stride must be >= D + R and a multiple of 8");
+  rolaq::AssembleArgs a{};
+  a.slots = slots;
+  a.n = n;
+  a.codes = codes;
+  a.params = params;
+  a.rope = static_cast<const uint16_t*>(rope_buf);
+  a.hp = static_cast<const uint16_t*>(hp_c);
+  a.row_of_slot = row_of_slot;
+  a.owner_of_row = owner_of_row;
+  a.rot = static_cast<const uint16_t*>(rotation);
+  a.R = R;
+  a.out = static_cast<uint16_t*>(out);
+  a.out_st = out_stride;
+  return hip_status(rolaq_launch_assemble(a, D, static_cast<hipStream_t>(stream)), "assemble_rows launch");
+}
+
 }  // extern "C"
+
 

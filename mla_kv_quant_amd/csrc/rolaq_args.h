@@ -82,6 +82,21 @@ struct ExtendArgs {
   int64_t o_st, o_sh;
 };
 
+struct AssembleArgs {
+  const int64_t* slots;       // [n] token slots
+  int64_t n;
+  const uint8_t* codes;
+  const float* params;
+  const uint16_t* rope;
+  const uint16_t* hp;
+  const int32_t* row_of_slot;
+  const int32_t* owner_of_row;
+  const uint16_t* rot;        // R_eff [D, D] bf16 row-major, or null (rotated frame)
+  int R;
+  uint16_t* out;              // [n, out_st] bf16: latent (D) then rope (R)
+  int64_t out_st;
+};
+
 }  // namespace rolaq
 
 // Host launchers (defined next to their kernels).
@@ -99,3 +114,4 @@ hipError_t rolaq_launch_prepare_splits(const int32_t* splits, int32_t* quant, in
                                        hipStream_t stream);
 hipError_t rolaq_launch_writer(const rolaq::WriterArgs& a, int D, int num_cus, hipStream_t stream);
 hipError_t rolaq_launch_extend(const rolaq::ExtendArgs& a, int D, int R, int max_q_len, hipStream_t stream);
+hipError_t rolaq_launch_assemble(const rolaq::AssembleArgs& a, int D, hipStream_t stream);

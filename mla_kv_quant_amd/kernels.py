@@ -263,3 +263,33 @@ def extend_fwd(q: torch.Tensor, k_chunk: torch.Tensor, qo_indptr: torch.Tensor, 
         _p(hp_c), B, H, D, R, int(P), int(W), int(max_q_len), float(sm_scale), _p(out), out.stride(0),
         out.stride(1), _stream(q)))
     return out
+
+
+def assemble_rows(slots: torch.Tensor, codes: torch.Tensor, params: torch.Tensor, rope_buf: torch.Tensor,
+                  hp_c: torch.Tensor, row_of_slot: torch.Tensor, owner_of_row: torch.Tensor,
+                  rotation: torch.Tensor | None, out: torch.Tensor) -> torch.Tensor:
+    """Cache rows at ``slots`` as bf16 ``[n, D + R]`` (latent, optionally un-rotated, then rope)."""
+    dev = codes.device
+    _need(slots, "slots", torch.int64, dev, 1)
+    _contig(slots, "slots")
+    D = codes.shape[1] * 4
+    R = rope_buf.shape[1]
+    for name, t, dt in (("codes", codes, torch.uint8), ("params", params, torch.float32),
+                        ("rope_buf", rope_buf, torch.bfloat16), ("hp_c", hp_c, torch.bfloat16),
+                        ("row_of_slot", row_of_slot, torch.int32), ("owner_of_row", owner_of_row, torch.int32)):
+        _need(t, name, dt, dev)
+        _contig(t, name)
+    if hp_c.shape[1] != D or tuple(params.shape[1:]) != (D // GROUP_SIZE, 2):
+        raise ValueError("cache buffers do not match")
+    if rotation is not None:
+        _need(rotation, "rotation", torch.bfloat16, dev, 2)
+        _contig(rotation, "rotation")
+        if tuple(rotation.shape) != (D, D):
+            raise ValueError("rotation must be [D, D]")
+    _need(out, "out", torch.bfloat16, dev, 2)
+    if out.shape[0] < slots.numel() or out.shape[1] < D + R or out.stride(1) != 1:
+        raise ValueError("out must be [n, >= D + R] with a contiguous last dim")
+    _lib.check(_lib.load().rolaq_assemble_rows(
+        _p(slots), slots.numel(), _p(codes), _p(params), _p(rope_buf), _p(hp_c), _p(row_of_slot),
+        _p(owner_of_row), _p(rotation), D, R, _p(out), out.stride(0), _stream(codes)))
+    return out

@@ -19,7 +19,8 @@ def declared_symbols():
 def test_header_declares_the_entry_points():
     syms = declared_symbols()
     for name in ("rolaq_last_error", "rolaq_abi_version", "rolaq_scatter_pack_rows", "rolaq_write_rows",
-                 "rolaq_prepare_gf_splits", "rolaq_decode_fwd", "rolaq_decode_partials", "rolaq_decode_merge", "rolaq_extend_fwd"):
+                 "rolaq_prepare_gf_splits", "rolaq_decode_fwd", "rolaq_decode_partials", "rolaq_decode_merge", "rolaq_extend_fwd",
+                 "rolaq_assemble_rows"):
         assert name in syms
 
 
@@ -80,6 +81,20 @@ def test_invalid_arguments_are_rejected_before_any_launch():
     bad = list(eargs)
     bad[15] = 0
     assert lib.rolaq_extend_fwd(*bad) == _lib.ROLAQ_OK
+    # assemble: shapes, strides, pointers; n == 0 is a no-op
+    aargs = [p, 10, p, p, p, p, p, p, None, 512, 64, p, 576, None]
+    bad = list(aargs)
+    bad[9], bad[10] = 512, 32
+    assert lib.rolaq_assemble_rows(*bad) == _lib.ROLAQ_ERR_INVALID and b"(D, R)" in lib.rolaq_last_error()
+    bad = list(aargs)
+    bad[12] = 500
+    assert lib.rolaq_assemble_rows(*bad) == _lib.ROLAQ_ERR_INVALID and b"stride" in lib.rolaq_last_error()
+    bad = list(aargs)
+    bad[0] = None
+    assert lib.rolaq_assemble_rows(*bad) == _lib.ROLAQ_ERR_INVALID
+    bad = list(aargs)
+    bad[1] = 0
+    assert lib.rolaq_assemble_rows(*bad) == _lib.ROLAQ_OK
 
 
 def test_check_raises_value_error():
