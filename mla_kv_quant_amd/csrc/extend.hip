@@ -15,8 +15,9 @@
 // scores and the latent transposed for the output -- while the previous tile
 // is being consumed, double-buffered. Per wave and tile:
 //   S^T[32 keys, RW rows] = K . Q^T   on MFMA 16x16x32 (Q held in registers)
-//   online softmax in the log2 domain, lazy rescaling (the running maximum is
-//   only moved when a tile exceeds it by more than 2^8)
+//   softmax in the log2 domain against a fixed per-row reference (the row's
+//   maximum over the first tile); a block whose scores exceed it by more than
+//   2^64 somewhere is redone with the true maxima, so O is never rescaled
 //   O[RW rows, D] += P . V           on MFMA 16x16x32, the keys of each lane
 //                                     taken in the order the score MFMA left them,
 //                                     P split into bf16 hi + lo (FP32-level accuracy).
@@ -26,7 +27,7 @@
 namespace rolaq {
 
 constexpr int kExtKeys = 32;          // keys per tile
-constexpr float kExtLazy = 8.0f;      // log2 slack before the running max moves
+constexpr float kExtSlack = 64.0f;    // log2 headroom of a score over the softmax reference
 constexpr float kExtMasked = -1.0e30f;
 
 template <int D, int R>
@@ -63,56 +64,76 @@ __device__ __forceinline__ float add_over_rows(float v) {
 template <int D, int R>
 struct TileRaw {
   static constexpr int OPT = ExtGeo<D, R>::OPT;
-  u32x4 lat[4][OPT];  // bf16 rows, or the codes of the octets in lat[k][0].x
+  u32x4 lat[4][OPT];  // bf16 rows
+  uint32_t code[4];   // packed codes of the thread's octets (INT2 rows)
   u32x4 rope[4];      // rope octet o (threads o < R / 8)
   f32x2 prm[4];       // (scale, zero) of the INT2 rows' group
   uint32_t mode;      // 2 bits per key: 0 zero, 1 bf16, 2 int2
 };
 
+// Pages of the prefix keys of a tile (page-table lookups), one tile ahead of
+// the data loads; the values are first used by the next tile's load_tile, so
+// no instruction of this tile waits on them (0 for keys without a page).
 template <int D, int R>
-__device__ __forceinline__ void load_tile(const ExtendArgs& a, TileRaw<D, R>& t, int k0, int kq, int o,
-                                          int64_t qo0, int64_t prefix, int64_t L, int64_t req,
-                                          int64_t kv0, int kend) {
-  constexpr int NG = D / 128, OPT = ExtGeo<D, R>::OPT;
-  t.mode = 0;
+__device__ __forceinline__ void lookup_tile(const ExtendArgs& a, int32_t pg[4], int k0, int kq, int64_t prefix,
+                                            int64_t kv0, int kend) {
 #pragma unroll
   for (int k = 0; k < 4; ++k) {
     const int kp = k0 + 4 * kq + k;
+    pg[k] = (kp < kend && kp < prefix) ? gload<int32_t>(a.kv_indices + kv0 + (kp >> a.page_shift)) : 0;
+  }
+}
+
+template <int D, int R>
+__device__ __forceinline__ void load_tile(const ExtendArgs& a, TileRaw<D, R>& t, const int32_t pg[4], int k0,
+                                          int kq, int o, int64_t qo0, int64_t prefix, int64_t L, int64_t req,
+                                          int kend) {
+  constexpr int NG = D / 128, OPT = ExtGeo<D, R>::OPT;
+  const int dlo = 8 * OPT * o;  // first latent column of this thread
+  const int g = dlo / 128, e0 = dlo % 128;
+  // where each key's bytes are (all addresses first: the pages were loaded an
+  // iteration ago, and no load below may wait behind another)
+  const uint16_t* lat[4];
+  const uint16_t* rope[4];
+  const uint8_t* code[4];
+  const float* prm[4];
+  uint32_t mode = 0;
 #pragma unroll
-    for (int j = 0; j < OPT; ++j) t.lat[k][j] = u32x4{0u, 0u, 0u, 0u};
-    t.rope[k] = u32x4{0u, 0u, 0u, 0u};
-    t.prm[k] = f32x2{0.f, 0.f};
+  for (int k = 0; k < 4; ++k) {
+    const int kp = k0 + 4 * kq + k;
+    const int64_t slot = (int64_t)pg[k] * (1 << a.page_shift) + (kp & ((1 << a.page_shift) - 1));
+    lat[k] = nullptr;
+    rope[k] = nullptr;
+    code[k] = nullptr;
+    prm[k] = nullptr;
     if (kp >= kend) continue;
-    const int dlo = 8 * OPT * o;  // first latent column of this thread
-    if (kp >= prefix) {
-      // a row of the chunk itself: the given BF16 key
-      const uint16_t* src = a.kc + (qo0 + kp - prefix) * a.kc_st;
-#pragma unroll
-      for (int j = 0; j < OPT; ++j) t.lat[k][j] = *reinterpret_cast<const u32x4*>(src + dlo + 8 * j);
-      if (o < R / 8) t.rope[k] = *reinterpret_cast<const u32x4*>(src + D + 8 * o);
-      t.mode |= 1u << (2 * k);
-      continue;
-    }
-    const int64_t slot = (int64_t)a.kv_indices[kv0 + (kp >> a.page_shift)] * (1 << a.page_shift) +
-                         (kp & ((1 << a.page_shift) - 1));
-    if (o < R / 8) t.rope[k] = *reinterpret_cast<const u32x4*>(a.rope + slot * R + 8 * o);
-    if (kp < a.P || kp >= L - a.W) {
+    if (kp >= prefix) {  // a row of the chunk itself: the given BF16 key
+      lat[k] = a.kc + (qo0 + kp - prefix) * a.kc_st + dlo;
+      rope[k] = a.kc + (qo0 + kp - prefix) * a.kc_st + D + 8 * o;
+      mode |= 1u << (2 * k);
+    } else if (kp < a.P || kp >= L - a.W) {  // BF16 window row
       const int inner = kp < a.P ? kp : a.P + (kp - a.P) % (a.W > 0 ? a.W : 1);
-      const uint16_t* src = a.hp + (1 + req * (a.P + a.W) + inner) * D;
-#pragma unroll
-      for (int j = 0; j < OPT; ++j) t.lat[k][j] = *reinterpret_cast<const u32x4*>(src + dlo + 8 * j);
-      t.mode |= 1u << (2 * k);
-    } else {
-      const int g = dlo / 128, e0 = dlo % 128;
-      const uint8_t* crow = a.codes + slot * (D / 4) + 4 * (NG * (e0 / 16) + g);
-      if constexpr (OPT == 2) {
-        t.lat[k][0].x = *reinterpret_cast<const uint32_t*>(crow);
-      } else {
-        t.lat[k][0].x = *reinterpret_cast<const uint16_t*>(crow + 2 * ((e0 / 8) & 1));
-      }
-      t.prm[k] = *reinterpret_cast<const f32x2*>(a.params + slot * 2 * NG + 2 * g);
-      t.mode |= 2u << (2 * k);
+      lat[k] = a.hp + (1 + req * (a.P + a.W) + inner) * D + dlo;
+      rope[k] = a.rope + slot * R + 8 * o;
+      mode |= 1u << (2 * k);
+    } else {  // INT2 row
+      code[k] = a.codes + slot * (D / 4) + 4 * (NG * (e0 / 16) + g) + (OPT == 2 ? 0 : 2 * ((e0 / 8) & 1));
+      prm[k] = a.params + slot * 2 * NG + 2 * g;
+      rope[k] = a.rope + slot * R + 8 * o;
+      mode |= 2u << (2 * k);
     }
+  }
+  t.mode = mode;
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int k = 0; k < 4; ++k) {
+    const uint32_t m = (mode >> (2 * k)) & 3u;
+#pragma unroll
+    for (int j = 0; j < OPT; ++j) t.lat[k][j] = m == 1u ? gload<u32x4>(lat[k] + 8 * j) : u32x4{0u, 0u, 0u, 0u};
+    if constexpr (OPT == 2) t.code[k] = m == 2u ? gload<uint32_t>(code[k]) : 0u;
+    else t.code[k] = m == 2u ? uint32_t(gload<uint16_t>(code[k])) : 0u;
+    t.prm[k] = m == 2u ? gload<f32x2>(prm[k]) : f32x2{0.f, 0.f};
+    t.rope[k] = (m != 0u && o < R / 8) ? gload<u32x4>(rope[k]) : u32x4{0u, 0u, 0u, 0u};
   }
 }
 
@@ -134,7 +155,7 @@ __device__ __forceinline__ void store_tile(const TileRaw<D, R>& t, uint8_t* buf,
       const uint32_t m = (t.mode >> (2 * k)) & 3u;
       if (m == 2u) {
         // (code - zero) * scale, rounded to bf16 as the reference's QDQ rows are
-        const uint32_t bits = OPT == 2 ? (t.lat[k][0].x >> (16 * j)) : t.lat[k][0].x;
+        const uint32_t bits = OPT == 2 ? (t.code[k] >> (16 * j)) : t.code[k];
         const float sc = t.prm[k].x, z = t.prm[k].y;
         float f[8];
 #pragma unroll
@@ -207,123 +228,131 @@ __global__ __launch_bounds__(256, 1) void extend_kernel(ExtendArgs a) {
       qf[nb][ks] = ok ? *reinterpret_cast<const u32x4*>(qr + 32 * ks) : u32x4{0u, 0u, 0u, 0u};
   }
 
-  f32x4 acc_o[NBR][ND];
-#pragma unroll
-  for (int nb = 0; nb < NBR; ++nb)
-#pragma unroll
-    for (int nd = 0; nd < ND; ++nd) acc_o[nb][nd] = f32x4{0.f, 0.f, 0.f, 0.f};
-  float m_run[NBR], l_run[NBR];
-#pragma unroll
-  for (int nb = 0; nb < NBR; ++nb) {
-    m_run[nb] = kExtMasked;
-    l_run[nb] = 0.f;
-  }
   const float c2 = a.sm_scale * kLog2e;
+  int qp[NBR];  // causal limit of each lane's rows (-1: no row)
+#pragma unroll
+  for (int nb = 0; nb < NBR; ++nb) qp[nb] = (int)qpos[nb];
 
-  TileRaw<D, R> raw;
-  load_tile<D, R>(a, raw, 0, kq, o, qo0, prefix, L, req, kv0, kend);
-  store_tile<D, R>(raw, s_buf, kq, o);
-  if (ntiles > 1) load_tile<D, R>(a, raw, kExtKeys, kq, o, qo0, prefix, L, req, kv0, kend);
-  __syncthreads();
-
-  for (int it = 0; it < ntiles; ++it) {
-    const uint8_t* kb = s_buf + (it & 1) * G::BUF;
-    const uint8_t* vb = kb + G::KBYTES;
-    const int k0 = it * kExtKeys;
-
-    // ---- scores S^T[key, row] ----------------------------------------------
-    f32x4 s[2][NBR];
-#pragma unroll
-    for (int mk = 0; mk < 2; ++mk)
-#pragma unroll
-      for (int nb = 0; nb < NBR; ++nb) s[mk][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int ks = 0; ks < KSQ; ++ks) {
-#pragma unroll
-      for (int mk = 0; mk < 2; ++mk) {
-        const u32x4 kf = *reinterpret_cast<const u32x4*>(kb + (16 * mk + la) * G::KSTR + 64 * ks + 16 * gq);
-#pragma unroll
-        for (int nb = 0; nb < NBR; ++nb) s[mk][nb] = mfma16x16x32(kf, qf[nb][ks], s[mk][nb]);
-      }
-    }
-
-    // ---- online softmax (row = 16 nb + la; keys 16 mk + 4 gq + i) -------------
-    u32x4 pf[NBR], pl[NBR];
-    bool need = false;
-    float tmax[NBR];
+  f32x4 acc_o[NBR][ND];
+  float m_ref[NBR], m_lane[NBR], l_run[NBR];
+  bool redo = false;
+  for (int pass = 0; pass < 2; ++pass) {
 #pragma unroll
     for (int nb = 0; nb < NBR; ++nb) {
-      float mx = kExtMasked;
 #pragma unroll
-      for (int mk = 0; mk < 2; ++mk)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int kp = k0 + 16 * mk + 4 * gq + i;
-          const float v = kp <= qpos[nb] ? s[mk][nb][i] * c2 : kExtMasked;
-          s[mk][nb][i] = v;
-          mx = fmaxf(mx, v);
-        }
-      tmax[nb] = max_over_rows(mx);
-      need |= tmax[nb] > m_run[nb] + kExtLazy;
-    }
-    if (__any(need)) {
-#pragma unroll
-      for (int nb = 0; nb < NBR; ++nb) {
-        const float mn = fmaxf(m_run[nb], tmax[nb]);
-        const float f = __builtin_amdgcn_exp2f(m_run[nb] - mn);
-        m_run[nb] = mn;
-        l_run[nb] *= f;
-        // rows 16 nb + 4 gq + i of the output layout live in lanes 4 gq + i
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float fi = __int_as_float(__builtin_amdgcn_ds_bpermute(4 * (4 * gq + i), __float_as_int(f)));
-#pragma unroll
-          for (int nd = 0; nd < ND; ++nd) acc_o[nb][nd][i] *= fi;
-        }
-      }
-    }
-#pragma unroll
-    for (int nb = 0; nb < NBR; ++nb) {
-      float p[2][4];
-#pragma unroll
-      for (int mk = 0; mk < 2; ++mk)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float v = s[mk][nb][i];
-          p[mk][i] = v > kExtMasked ? __builtin_amdgcn_exp2f(v - m_run[nb]) : 0.f;
-          l_run[nb] += p[mk][i];
-        }
-      // P as bf16 hi + lo: the output keeps FP32-level accuracy in P
-      pf[nb] = u32x4{pack_bf16(p[0][0], p[0][1]), pack_bf16(p[0][2], p[0][3]), pack_bf16(p[1][0], p[1][1]),
-                     pack_bf16(p[1][2], p[1][3])};
-      float r[2][4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const uint32_t w = pf[nb][e];
-        r[e >> 1][2 * (e & 1)] = p[e >> 1][2 * (e & 1)] - bf16_lo(w);
-        r[e >> 1][2 * (e & 1) + 1] = p[e >> 1][2 * (e & 1) + 1] - bf16_hi(w);
-      }
-      pl[nb] = u32x4{pack_bf16(r[0][0], r[0][1]), pack_bf16(r[0][2], r[0][3]), pack_bf16(r[1][0], r[1][1]),
-                     pack_bf16(r[1][2], r[1][3])};
+      for (int nd = 0; nd < ND; ++nd) acc_o[nb][nd] = f32x4{0.f, 0.f, 0.f, 0.f};
+      m_lane[nb] = kExtMasked;
+      l_run[nb] = 0.f;
     }
 
-    // ---- O[row, d] += P . V --------------------------------------------------
-#pragma unroll
-    for (int nd = 0; nd < ND; ++nd) {
-      const u32x4 vf = *reinterpret_cast<const u32x4*>(vb + (16 * nd + la) * G::VSTR + 16 * gq);
-#pragma unroll
-      for (int nb = 0; nb < NBR; ++nb) {
-        acc_o[nb][nd] = mfma16x16x32(pf[nb], vf, acc_o[nb][nd]);
-        acc_o[nb][nd] = mfma16x16x32(pl[nb], vf, acc_o[nb][nd]);
-      }
-    }
-
-    // ---- next tile: store the one loaded, load the one after -----------------
-    if (it + 1 < ntiles) {
-      store_tile<D, R>(raw, s_buf + ((it + 1) & 1) * G::BUF, kq, o);
-      if (it + 2 < ntiles) load_tile<D, R>(a, raw, (it + 2) * kExtKeys, kq, o, qo0, prefix, L, req, kv0, kend);
-    }
+    TileRaw<D, R> raw;
+    int32_t sl[4];
+    lookup_tile<D, R>(a, sl, 0, kq, prefix, kv0, kend);
+    load_tile<D, R>(a, raw, sl, 0, kq, o, qo0, prefix, L, req, kend);
+    lookup_tile<D, R>(a, sl, kExtKeys, kq, prefix, kv0, kend);
+    store_tile<D, R>(raw, s_buf, kq, o);
     __syncthreads();
+
+    for (int it = 0; it < ntiles; ++it) {
+      const uint8_t* kb = s_buf + (it & 1) * G::BUF;
+      const uint8_t* vb = kb + G::KBYTES;
+      const int k0 = it * kExtKeys;
+      // loads of the next tile first: they have this tile's compute to land
+      // (its pages were looked up an iteration ago)
+      if (it + 1 < ntiles) {
+        load_tile<D, R>(a, raw, sl, k0 + kExtKeys, kq, o, qo0, prefix, L, req, kend);
+        lookup_tile<D, R>(a, sl, k0 + 2 * kExtKeys, kq, prefix, kv0, kend);
+      }
+
+      // ---- scores S^T[key, row] --------------------------------------------
+      f32x4 s[2][NBR];
+#pragma unroll
+      for (int mk = 0; mk < 2; ++mk)
+#pragma unroll
+        for (int nb = 0; nb < NBR; ++nb) s[mk][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < KSQ; ++ks) {
+#pragma unroll
+        for (int mk = 0; mk < 2; ++mk) {
+          const u32x4 kf = *reinterpret_cast<const u32x4*>(kb + (16 * mk + la) * G::KSTR + 64 * ks + 16 * gq);
+#pragma unroll
+          for (int nb = 0; nb < NBR; ++nb) s[mk][nb] = mfma16x16x32(kf, qf[nb][ks], s[mk][nb]);
+        }
+      }
+
+      // ---- softmax against the fixed reference (row = 16 nb + la; keys 16 mk + 4 gq + i)
+#pragma unroll
+      for (int nb = 0; nb < NBR; ++nb) {
+        float mx = m_lane[nb];
+#pragma unroll
+        for (int mk = 0; mk < 2; ++mk)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int kp = k0 + 16 * mk + 4 * gq + i;
+            const float v = kp <= qp[nb] ? s[mk][nb][i] * c2 : kExtMasked;
+            s[mk][nb][i] = v;
+            mx = fmaxf(mx, v);
+          }
+        m_lane[nb] = mx;
+      }
+      // the reference of the first pass: each row's maximum over the first tile
+      // (key 0 is visible to every row, so it is finite)
+      if (it == 0 && pass == 0) {
+#pragma unroll
+        for (int nb = 0; nb < NBR; ++nb) m_ref[nb] = max_over_rows(m_lane[nb]);
+      }
+      u32x4 pf[NBR], pl[NBR];
+#pragma unroll
+      for (int nb = 0; nb < NBR; ++nb) {
+        float p[2][4];
+#pragma unroll
+        for (int mk = 0; mk < 2; ++mk)
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            p[mk][i] = __builtin_amdgcn_exp2f(s[mk][nb][i] - m_ref[nb]);  // masked: 2^-1e30 = 0
+            l_run[nb] += p[mk][i];
+          }
+        // P as bf16 hi + lo: the output keeps FP32-level accuracy in P
+        pf[nb] = u32x4{pack_bf16(p[0][0], p[0][1]), pack_bf16(p[0][2], p[0][3]), pack_bf16(p[1][0], p[1][1]),
+                       pack_bf16(p[1][2], p[1][3])};
+        float r[2][4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t w = pf[nb][e];
+          r[e >> 1][2 * (e & 1)] = p[e >> 1][2 * (e & 1)] - bf16_lo(w);
+          r[e >> 1][2 * (e & 1) + 1] = p[e >> 1][2 * (e & 1) + 1] - bf16_hi(w);
+        }
+        pl[nb] = u32x4{pack_bf16(r[0][0], r[0][1]), pack_bf16(r[0][2], r[0][3]), pack_bf16(r[1][0], r[1][1]),
+                       pack_bf16(r[1][2], r[1][3])};
+      }
+
+      // ---- O[row, d] += P . V ------------------------------------------------
+#pragma unroll
+      for (int nd = 0; nd < ND; ++nd) {
+        const u32x4 vf = *reinterpret_cast<const u32x4*>(vb + (16 * nd + la) * G::VSTR + 16 * gq);
+#pragma unroll
+        for (int nb = 0; nb < NBR; ++nb) {
+          acc_o[nb][nd] = mfma16x16x32(pf[nb], vf, acc_o[nb][nd]);
+          acc_o[nb][nd] = mfma16x16x32(pl[nb], vf, acc_o[nb][nd]);
+        }
+      }
+
+      // ---- next tile into the other buffer (last read before the previous barrier)
+      if (it + 1 < ntiles) store_tile<D, R>(raw, s_buf + ((it + 1) & 1) * G::BUF, kq, o);
+      __syncthreads();
+    }
+
+    // a score above the reference by more than the slack (2^64 bounds every P
+    // and keeps the sums finite): redo the block with each row's true maximum
+    bool over = false;
+#pragma unroll
+    for (int nb = 0; nb < NBR; ++nb) {
+      const float mt = max_over_rows(m_lane[nb]);
+      over |= mt > m_ref[nb] + kExtSlack;
+      m_ref[nb] = mt;
+    }
+    redo = __syncthreads_or(pass == 0 && over);
+    if (!redo) break;
   }
 
   // ---- normalise and store -----------------------------------------------------

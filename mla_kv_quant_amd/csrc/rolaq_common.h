@@ -41,6 +41,14 @@ __device__ __forceinline__ uint16_t float_to_bf16(float f) {
   return uint16_t(pack_bf16(f, 0.0f) & 0xffffu);
 }
 
+// Load through a global (address space 1) pointer: a global_load, which only
+// vmcnt tracks. A load through a generic pointer becomes flat_load, which LDS
+// waits (lgkmcnt) must also drain.
+template <typename T>
+__device__ __forceinline__ T gload(const void* p) {
+  return *(const __attribute__((address_space(1))) T*)(p);
+}
+
 // In-place unpack of one packed word (16 codes; code p at bits 2p) into eight
 // dwords of two bf16 each. Dword k holds (code k, code k + 8) as the bf16
 // values 4 + c * 2^(e_k - 5), e = {0, 2, 4, 0, 2, 4, 0, 2}: the code bits are

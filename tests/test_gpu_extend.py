@@ -30,7 +30,7 @@ CASES = [
 ]
 
 
-def run_case(D, R, H, prefixes, chunks, page, seed):
+def run_case(D, R, H, prefixes, chunks, page, seed, kc_scale=1.0):
     P, W = 4, 16
     sm = 1.0 / math.sqrt(96 if D == 256 else 192)
     pool, slots, pages, reqs, _ = build_pool(prefixes, D, R, P, W, page, seed=seed)
@@ -39,8 +39,8 @@ def run_case(D, R, H, prefixes, chunks, page, seed):
     T = sum(chunks)
     sigma = 2.0 / (sm * math.sqrt(D + R))
     q = synth.make_normal((T, H, D + R), seed + 1, std=sigma)
-    kc = torch.cat([synth.make_latent(T, D, 3, seed=seed + 2),
-                    synth.make_normal((T, R), seed + 3)], 1).to(torch.bfloat16)
+    kc = (kc_scale * torch.cat([synth.make_latent(T, D, 3, seed=seed + 2),
+                                synth.make_normal((T, R), seed + 3)], 1)).to(torch.bfloat16)
     qo = np.zeros(B + 1, np.int32)
     qo[1:] = np.cumsum(chunks)
     indptr, indices = index_lists(slots, pages, page)
@@ -73,4 +73,14 @@ def test_extend_single_token_chunk_equals_decode_semantics():
     D, R, H, P, W, page = 256, 32, 40, 4, 16, 16
     L = 700
     out, ref = run_case(D, R, H, [L - 1], [1], page, seed=3)
+    torch.testing.assert_close(out.double(), ref, rtol=RTOL, atol=ATOL)
+
+
+def test_extend_redo_when_scores_outgrow_the_first_tile():
+    """The chunk's keys scaled 40x put later scores far above every row's
+    first-tile maximum (beyond the kernel's 2^64 headroom), so blocks take the
+    second pass with the true maxima; the result must still match."""
+    D, R, H, page = 256, 32, 8, 16
+    out, ref = run_case(D, R, H, [40, 100], [50, 30], page, seed=11, kc_scale=40.0)
+    assert torch.isfinite(out).all()
     torch.testing.assert_close(out.double(), ref, rtol=RTOL, atol=ATOL)
