@@ -12,6 +12,10 @@ Also reported (``writer``): the fused cache writer at config 1 -- 64 sequences
 x 2048-token prefill chunk, 27 layers with their own buffers -- in Mtokens/s
 (token-layers per second) and as a fraction of HBM peak.
 
+Also reported (``reported``): decode at config 3 (batch 128, ragged context
+U[2048, 8192], shuffled pages) and config 4a (MiniCPM3 shape: 40 heads, latent
+256, batch 64 x 16384), 4 layers each with their own buffers.
+
 ``roofline``: algorithmic bytes per decode layer (288 B per INT2 token, window
 rows, q and out) over the measured layer time, against 8 TB/s. ``traffic`` is
 taken from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary when present.
@@ -53,6 +57,8 @@ def parse():
     ap.add_argument("--writer-only", action="store_true", help="only the cfg1 writer (prints its own JSON)")
     ap.add_argument("--extend-only", action="store_true", help="only the cfg4b extend (prints its own JSON)")
     ap.add_argument("--no-extend", action="store_true")
+    ap.add_argument("--no-reported", action="store_true", help="skip the cfg3 / cfg4a decode lines")
+    ap.add_argument("--reported-only", action="store_true", help="only the cfg3 / cfg4a decode lines")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only time a 1 GiB device copy (the reference kernel for rocprofv3 byte counters)")
     return ap.parse_args()
@@ -62,33 +68,41 @@ def parse():
 # config 2: decode
 # ---------------------------------------------------------------------------
 class DecodeBench:
+    """A decode workload: per-layer caches written by the fused writer, a shuffled page table."""
+
     B, L, H, D, R, P, W, PAGE = 32, 16384, 16, 512, 64, 4, 16, 64
 
-    def __init__(self, layers: int, dev: str):
+    def __init__(self, layers: int, dev: str, B: int | None = None, lengths=None, H: int | None = None,
+                 D: int | None = None, R: int | None = None, seed: int = 0):
         from mla_kv_quant_amd import kernels, synth
 
+        self.B = B or self.B
+        self.H, self.D, self.R = H or self.H, D or self.D, R or self.R
         self.layers, self.dev = layers, dev
-        B, L, D, R, P, W, PAGE = self.B, self.L, self.D, self.R, self.P, self.W, self.PAGE
-        pages_per_seq = L // PAGE
-        npages = B * pages_per_seq
-        rng = np.random.default_rng(0)
+        B, D, R, P, W, PAGE = self.B, self.D, self.R, self.P, self.W, self.PAGE
+        self.lengths = np.asarray(lengths if lengths is not None else [self.L] * B, dtype=np.int64)
+        self.L = int(self.lengths.max())
+        pages_per_seq = (self.lengths + PAGE - 1) // PAGE
+        npages = int(pages_per_seq.sum())
+        rng = np.random.default_rng(seed)
         perm = rng.permutation(np.arange(1, npages + 1)).astype(np.int64)  # page 0 = padding
-        page_table = perm.reshape(B, pages_per_seq)
+        indptr = np.concatenate([[0], np.cumsum(pages_per_seq)])
         self.num_slots = (npages + 1) * PAGE
-        self.kv_indptr = torch.arange(0, B * pages_per_seq + 1, pages_per_seq, dtype=torch.int32, device=dev)
-        self.kv_indices = torch.from_numpy(page_table.reshape(-1).astype(np.int32)).to(dev)
-        self.seq_lens = torch.full((B,), L, dtype=torch.int64, device=dev)
+        self.kv_indptr = torch.from_numpy(indptr.astype(np.int32)).to(dev)
+        self.kv_indices = torch.from_numpy(perm.astype(np.int32)).to(dev)
+        self.seq_lens = torch.from_numpy(self.lengths).to(dev)
         self.req = torch.arange(1, B + 1, dtype=torch.int64, device=dev)
-        slots = (torch.from_numpy(page_table).to(dev)[:, :, None] * PAGE
-                 + torch.arange(PAGE, device=dev)[None, None, :]).reshape(B, L)
-        positions = torch.arange(L, device=dev).repeat(B)
-        seqs = torch.full((B * L,), L, dtype=torch.int64, device=dev)
-        reqs = self.req.repeat_interleave(L)
-        loc = slots.reshape(-1).contiguous()
+        loc = torch.cat([(torch.from_numpy(perm[indptr[b]:indptr[b + 1]]).to(dev)[:, None] * PAGE
+                          + torch.arange(PAGE, device=dev)).reshape(-1)[: self.lengths[b]] for b in range(B)])
+        positions = torch.cat([torch.arange(int(n), device=dev) for n in self.lengths])
+        lens_t = torch.from_numpy(self.lengths).to(dev)
+        seqs = lens_t.repeat_interleave(lens_t)
+        reqs = self.req.repeat_interleave(lens_t)
+        n = int(self.lengths.sum())
         max_reqs = B + 1
         hp_rows = 1 + max_reqs * (P + W)
         self.caches = []
-        self.sm_scale = 1.0 / math.sqrt(192)
+        self.sm_scale = 1.0 / math.sqrt(192 if D == 512 else 96)
         sigma = 2.0 / (self.sm_scale * math.sqrt(D + R))
         for layer in range(layers):
             c = {
@@ -100,8 +114,8 @@ class DecodeBench:
                 "owner": torch.zeros(hp_rows, dtype=torch.int32, device=dev),
             }
             rt = synth.layer_rotation(D, layer).to(torch.bfloat16).t().contiguous().to(dev)
-            x = synth.make_latent(B * L, D, max(1, D // 100), seed=10_000 + layer, device=dev)
-            pe = synth.make_normal((B * L, R), 20_000 + layer, device=dev)
+            x = synth.make_latent(n, D, max(1, D // 100), seed=10_000 + layer, device=dev)
+            pe = synth.make_normal((n, R), 20_000 + layer, device=dev)
             kernels.write_rows(x, pe, rt, loc, seqs, positions, reqs, c["codes"], c["params"], c["rope"],
                                c["hp"], c["row"], c["owner"], P, W, max_reqs,
                                synth.DEFAULT_THRESHOLD, synth.DEFAULT_GAIN)
@@ -137,15 +151,31 @@ class DecodeBench:
                                     self.logits, self.lse, self.sm_scale, self.P, self.W, self.PAGE)
 
     def bytes_per_layer(self, with_out: bool = True) -> float:
-        """Algorithmic bytes: 288 B per INT2 token, window rows, q (and the bf16 output)."""
-        B, L, P, W, D, R, H = self.B, self.L, self.P, self.W, self.D, self.R, self.H
-        int2 = B * (L - P - W) * (D // 4 + 8 * (D // 128) + 2 * R)
-        window = B * (P + W) * (2 * D + 2 * R)
+        """Algorithmic bytes: D/4 + 8 NG + 2 R per INT2 token (288 B at D=512), window rows, q (and the output)."""
+        B, P, W, D, R, H = self.B, self.P, self.W, self.D, self.R, self.H
+        lens = self.lengths
+        win = np.minimum(lens, P + W)
+        int2 = int((lens - win).sum()) * (D // 4 + 8 * (D // 128) + 2 * R)
+        window = int(win.sum()) * (2 * D + 2 * R)
         q_out = B * H * (D + R) * 2 + (B * H * D * 2 if with_out else 0)
         return float(int2 + window + q_out)
 
     def flops_per_layer(self) -> float:
-        return float(2 * self.B * self.L * self.H * (2 * self.D + self.R))
+        return float(2 * int(self.lengths.sum()) * self.H * (2 * self.D + self.R))
+
+    def pick_splits(self, candidates, layers_label: str = "") -> int:
+        best = None
+        for ns in candidates:
+            self.alloc_scratch(ns)
+            self.set_splits(ns)
+            ms = time_loop(self.step, 2, 1)
+            print(f"[bench] {layers_label}splits={ns}: {ms * 1000 / self.layers:.2f} us/layer", file=sys.stderr,
+                  flush=True)
+            if best is None or ms < best[1]:
+                best = (ns, ms)
+        self.alloc_scratch(best[0])
+        self.set_splits(best[0])
+        return best[0]
 
 
 def time_loop(fn, steps: int, warmup: int) -> float:
@@ -357,6 +387,41 @@ def copy_probe(nbytes: int = 1 << 30, reps: int = 10) -> float:
     return 2.0 * nbytes / (ms * 1e-3) / 1e9
 
 
+def reported_decode_result(args, dev: str, name: str) -> dict:
+    """cfg3 (ragged large batch) or cfg4a (MiniCPM3 shape) decode, 4 layers with their own buffers."""
+    layers = 4
+    if name == "cfg3":
+        lens = np.random.default_rng(3).integers(2048, 8193, size=128)
+        db = DecodeBench(layers, dev, B=128, lengths=lens, H=16, D=512, R=64, seed=3)
+        workload = "cfg3 decode: batch 128, ragged context U[2048,8192], 16 heads, latent 512, rope 64, page 64 shuffled"
+        cands = [2, 3, 4, 5, 6, 8]
+    else:
+        db = DecodeBench(layers, dev, B=64, lengths=[16384] * 64, H=40, D=256, R=32, seed=4)
+        workload = "cfg4a decode: batch 64 x context 16384, 40 heads, latent 256, rope 32, page 64 shuffled"
+        cands = [4, 5, 6, 8, 9]
+    ns = db.pick_splits(cands, f"{name} ")
+    ms = time_loop(db.step, max(5, args.steps // 2), args.warmup)
+    us = ms * 1000.0 / layers
+    ms1 = time_loop(db.step_partials, max(5, args.steps // 2), args.warmup)
+    us1 = ms1 * 1000.0 / layers
+    ach1 = db.bytes_per_layer(with_out=False) / (us1 * 1e-6) / 1e9
+    res = {
+        "workload": workload,
+        "us_per_layer": round(us, 3),
+        "hbm_frac_layer": round(db.bytes_per_layer() / (us * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
+        "stage1_us": round(us1, 3),
+        "stage1_gbs": round(ach1, 1),
+        "stage1_hbm_frac": round(ach1 / HBM_PEAK_GBS, 4),
+        "mfma_frac": round(db.flops_per_layer() / (us1 * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
+        "num_kv_splits": ns,
+        "tokens": int(db.lengths.sum()),
+    }
+    print(f"[bench] {name}: {us:.2f} us/layer, stage 1 {us1:.2f} us ({ach1:.0f} GB/s)", file=sys.stderr, flush=True)
+    del db
+    torch.cuda.empty_cache()
+    return res
+
+
 def writer_result(args, dev: str) -> dict:
     wb = WriterBench(args.layers, dev)
     wms = time_loop(wb.step, max(3, args.steps // 2), args.warmup)
@@ -399,21 +464,14 @@ def main():
     if args.extend_only:
         print(json.dumps(extend_result(args, dev)), flush=True)
         return
+    if args.reported_only:
+        print(json.dumps({k: reported_decode_result(args, dev, k) for k in ("cfg3", "cfg4a")}), flush=True)
+        return
     t_setup = time.time()
     db = DecodeBench(args.layers, dev)
     print(f"[bench] decode caches written for {args.layers} layers in {time.time() - t_setup:.1f}s", file=sys.stderr,
           flush=True)
-    candidates = [args.splits] if args.splits else [8, 9, 15, 16, 17, 33]
-    best = None
-    for ns in candidates:
-        db.alloc_scratch(ns)
-        db.set_splits(ns)
-        ms = time_loop(db.step, 2, 1)
-        print(f"[bench] splits={ns}: {ms * 1000 / args.layers:.2f} us/layer", file=sys.stderr, flush=True)
-        if best is None or ms < best[1]:
-            best = (ns, ms)
-    db.alloc_scratch(best[0])
-    db.set_splits(best[0])
+    ns_best = db.pick_splits([args.splits] if args.splits else [8, 9, 15, 16, 17, 33])
     ms = time_loop(db.step, args.steps, args.warmup)
     us_layer = ms * 1000.0 / args.layers
     bpl = db.bytes_per_layer()
@@ -442,7 +500,7 @@ def main():
         "config": {"workload": "cfg2 decode: batch 32 x context 16384, 16 heads, latent 512, rope 64, "
                                "s4r16 window, page 64 shuffled, 27 layers with own buffers",
                    "batch": db.B, "context": db.L, "heads": db.H, "layers": args.layers,
-                   "num_kv_splits": best[0]},
+                   "num_kv_splits": ns_best},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": read_traffic(),
                      "kernel": "decode_stage1<512,64,paged>", "us_per_launch": round(us_stage1, 3),
@@ -452,13 +510,15 @@ def main():
                      "frac_of_copy": round(achieved / copy_gbs, 4),
                      "mfma_frac": round(db.flops_per_layer() / (us_stage1 * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4)},
     }
-    if not args.no_writer or not args.no_extend:
+    if not args.no_writer or not args.no_extend or not args.no_reported:
         del db.caches
         torch.cuda.empty_cache()
     if not args.no_writer:
         result["writer"] = writer_result(args, dev)
     if not args.no_extend:
         result["extend"] = extend_result(args, dev)
+    if not args.no_reported:
+        result["reported"] = {k: reported_decode_result(args, dev, k) for k in ("cfg3", "cfg4a")}
     if not args.no_cpu:
         if not hasattr(db, "caches"):
             db = DecodeBench(1, dev)
