@@ -484,6 +484,14 @@ __global__ __launch_bounds__(kThreads, 2) void decode_stage1(DecodeArgs a) {
   auto phase1 = [&](int tile, uint8_t* tl) {
     const int p0 = tile * TILE;
     const int tA = 16 * wh + la;  // A-operand token of this lane
+    // The query's B operands are read one group ahead of their MFMAs (group
+    // g + 1 while group g computes): read next to its MFMA, each read's LDS
+    // latency would stall the accumulation chain.
+    u32x4 qop[2][4], qrp[KR];
+#pragma unroll
+    for (int kr = 0; kr < KR; ++kr) qrp[kr] = s_qr[kr][lane];
+#pragma unroll
+    for (int kbl = 0; kbl < 4; ++kbl) qop[0][kbl] = s_qs[0][kbl][lane];
     uint32_t cw[2 * NG];          // words s = 2gq (cw[g]) and 2gq+1 (cw[NG+g]) of token tA
     if constexpr (NG == 4) {
       const u32x4 v0 = lds128(tl + 16 * G::cslot(tA, 2 * gq));
@@ -494,10 +502,15 @@ __global__ __launch_bounds__(kThreads, 2) void decode_stage1(DecodeArgs a) {
       const u32x4 v0 = lds128(tl + 16 * G::cslot(tA, gq));
       cw[0] = v0.x; cw[1] = v0.y; cw[2] = v0.z; cw[3] = v0.w;
     }
+    u32x4 ropa[KR];
+    f32x2 qqv[NG];  // Qsum, 4 Q' of head la per group
+#pragma unroll
+    for (int kr = 0; kr < KR; ++kr) ropa[kr] = lds128(tl + G::OFF_R + 16 * G::rslot(tA, 4 * kr + gq));
+#pragma unroll
+    for (int g = 0; g < NG; ++g) qqv[g] = s_qq[g][la];
     f32x4 accr = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int kr = 0; kr < KR; ++kr)
-      accr = mfma16x16x32(lds128(tl + G::OFF_R + 16 * G::rslot(tA, 4 * kr + gq)), s_qr[kr][lane], accr);
+    for (int kr = 0; kr < KR; ++kr) accr = mfma16x16x32(ropa[kr], qrp[kr], accr);
     float s[4] = {accr[0], accr[1], accr[2], accr[3]};
     // C-layout tokens of this lane: 16wh + 4gq + j
 #pragma unroll
@@ -508,15 +521,20 @@ __global__ __launch_bounds__(kThreads, 2) void decode_stage1(DecodeArgs a) {
 #pragma unroll
       for (int gg = 0; gg < 2; ++gg) {
         const int g = 2 * gp + gg;
+        if (g + 1 < NG) {
+#pragma unroll
+          for (int kbl = 0; kbl < 4; ++kbl) qop[(g + 1) & 1][kbl] = s_qs[g + 1][kbl][lane];
+        }
+        __builtin_amdgcn_sched_barrier(0);
         uint32_t d0[8], d1[8];
         unpack_word_fast(cw[g], d0, vbase);
         unpack_word_fast(cw[NG + g], d1, vbase);
         const u32x4 kop[4] = {{d0[0], d0[1], d0[2], d0[3]}, {d0[4], d0[5], d0[6], d0[7]},
                               {d1[0], d1[1], d1[2], d1[3]}, {d1[4], d1[5], d1[6], d1[7]}};
-        const f32x2 qq = s_qq[g][la];  // Qsum, 4 Q' of head la
+        const f32x2 qq = qqv[g];
         f32x4 acc = {-qq.y, -qq.y, -qq.y, -qq.y};
 #pragma unroll
-        for (int kbl = 0; kbl < 4; ++kbl) acc = mfma16x16x32(kop[kbl], s_qs[g][kbl][lane], acc);
+        for (int kbl = 0; kbl < 4; ++kbl) acc = mfma16x16x32(kop[kbl], qop[g & 1][kbl], acc);
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const float scl = gg ? pv[j].z : pv[j].x;
