@@ -4,9 +4,12 @@ import numpy as np
 import pytest
 import torch
 
-from oracle import codec, layout, window
+import math
+
+from oracle import attention, codec, layout, window
 from mla_kv_quant_amd import PackedMLAPool, synth, writer
-from tests.helpers import bf16_np_to_torch
+from mla_kv_quant_amd.decode import packed_mla_decode_gf_fwd
+from tests.helpers import bf16_np_to_torch, make_queries
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -135,6 +138,29 @@ def test_fused_writer_prefill_then_decode(D, R):
         written = np.concatenate([np.array(s) for s in seq_slots])
         for li in range(layers):
             _compare_layer(pool, li, refs[li], written, 1e-4)
+    # decode over what the GPU writer stored, against the oracle over its own pool
+    # (requests below max_reqs: the last one has no ring rows; token slots)
+    H = 16
+    sm = 1.0 / math.sqrt(192 if D == 512 else 96)
+    nb = max_reqs - 1
+    lens = [L + 3 for L in lengths][:nb]
+    slots = [np.array(s, np.int64) for s in seq_slots][:nb]
+    q = make_queries(nb, H, D, R, sm, seed=9)
+    indptr = torch.tensor(np.concatenate([[0], np.cumsum(lens)]), dtype=torch.int32, device=DEV)
+    indices = torch.from_numpy(np.concatenate(slots).astype(np.int32)).to(DEV)
+    for li in range(layers):
+        o = torch.empty(nb, H, D, dtype=torch.bfloat16, device=DEV)
+        logits = torch.empty(nb, H, 9, D, device=DEV)
+        lse = torch.empty(nb, H, 9, device=DEV)
+        packed_mla_decode_gf_fwd(q.to(DEV), o, pool, li, indptr, indices,
+                                 torch.tensor([2, 3, 1, 4, 8], dtype=torch.int32, device=DEV), 8, logits, lse, sm,
+                                 seq_lens=torch.tensor(lens, device=DEV),
+                                 req_pool_indices=torch.arange(1, nb + 1, device=DEV))
+        torch.cuda.synchronize()
+        ref64, _ = attention.decode(refs[li], q[..., :D], q[..., D:], slots, lens, list(range(1, nb + 1)), P, W, sm,
+                                    D, "fp64")
+        # the GPU pool may differ from the oracle's by rare +-1 codes (the budget above)
+        torch.testing.assert_close(o.float().cpu().double(), ref64, rtol=2e-2, atol=2e-3)
 
 
 def test_fused_writer_unrotated_layer_and_fallbacks():
