@@ -12,10 +12,12 @@
 // nq + 1 partials by LSE.
 //
 // INT2 split arithmetic (per 32-token tile):
-//   scores  S^T[t, h] = sum_g scale_tg (sum_j q'_hj v_tj - 4 Q'_hg - zero_tg Qsum_hg)
-//           on bf16 MFMA 16x16x32 with M = 16 tokens, N = 16 heads, K = latent.
-//           v_tj = 4 + c_tj 2^(e-5) is the code masked into a bf16 mantissa and
-//           q'_hj = q_hj 2^(5-e) the matching exact rescale of the query.
+//   scores  S^T[t, h] = rope_th + 2^(1-kq_h) sum_g scale_tg (A_tgh - zero_tg Qsum_hg 2^(kq_h-1)),
+//           A_tgh = sum_j (c_tj / 2) q'_hj on the fp4 x fp8 MFMA 16x16x128 with
+//           M = 16 tokens, N = 16 heads, K = one quantization group: the code c
+//           masked into an e2m1 nibble (0b00cc = c / 2) and q'_h = q_h 2^kq_h as
+//           two e4m3 pieces (exact to 2^-10 of the head's largest |q|). The rope
+//           term is a bf16 MFMA 16x16x32.
 //   output  O[h, f] += sum_t p'_g[h,t] v_t[f] with p'_g = p * scale_tg, M = heads,
 //           N = 16 features, K = 32 tokens. The A operand is the softmax tile in
 //           the score accumulator's own lane layout; the B operand is built by a
@@ -294,7 +296,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_stage1(DecodeArgs a) {
   static_assert(R % 32 == 0 && D % 256 == 0, "unsupported shape");
   static_assert(8 * D * 4 <= RING, "merge buffer (8 heads) does not fit in one ring buffer");
   static_assert(window_half_rows_bytes<D, R>() <= RING && 4 * 16 * kMaxWindow * 4 <= RING &&
-                (16 * kMaxWindow + 16) * 4 <= NG * 4 * 64 * 16, "window scratch");
+                (16 * kMaxWindow + 16) * 4 <= NG * 4 * 64 * 16 && 16 * D * 2 <= RING, "window / query scratch");
   using Pages = TilePages<CLW, RLW, PAGED>;
 
   // Three tile buffers as separate LDS objects, so the compiler's wait
@@ -302,10 +304,11 @@ __global__ __launch_bounds__(kThreads, 2) void decode_stage1(DecodeArgs a) {
   __shared__ __attribute__((aligned(16))) uint8_t s_r0[RING];
   __shared__ __attribute__((aligned(16))) uint8_t s_r1[RING];
   __shared__ __attribute__((aligned(16))) uint8_t s_r2[RING];
-  // score-MFMA B operands of the query: [group][K-block][lane]
-  __shared__ __attribute__((aligned(16))) u32x4 s_qs[NG][4][64];
-  __shared__ __attribute__((aligned(16))) u32x4 s_qr[KR][64];  // rope B operands
-  __shared__ f32x2 s_qq[NG][16];           // per group and head: Qsum, 4 Q'
+  // score-MFMA B operands of the query (fp8 e4m3): [group][piece][half][lane]
+  __shared__ __attribute__((aligned(16))) u32x4 s_qs[NG][2][2][64];
+  __shared__ __attribute__((aligned(16))) u32x4 s_qr[KR][64];  // rope B operands (bf16)
+  __shared__ f32x2 s_qq[NG][16];           // per group and head: Qsum 2^(kq-1), 2^(1-kq)
+  __shared__ float s_qmax[NG][16];         // per group and head: max |q|
   __shared__ float s_ml[kPairs][16][2];    // per pair and head: reference max, sum
 
   const int nhg = (a.H + 15) / 16;
@@ -417,52 +420,104 @@ __global__ __launch_bounds__(kThreads, 2) void decode_stage1(DecodeArgs a) {
   uint8_t* const tb0 = s_r0 + pr * G::TILE_LDS;
   uint8_t* const tb1 = s_r1 + pr * G::TILE_LDS;
   uint8_t* const tb2 = s_r2 + pr * G::TILE_LDS;
+  // ---- query operands (wave w prepares groups w, w + 4, .. and rope K-block w) ---
+  // The query's global loads go out first, before the page lookups: they then
+  // complete together with the lookups instead of queueing behind the first
+  // tiles' direct loads (the memory counter drains in order).
+  constexpr int QG = (NG + 2 * kPairs - 1) / (2 * kPairs);  // groups per wave
+  const int hq = h0 + la;
+  const bool hv = hq < a.H;
+  const uint16_t* qh = a.q + b * a.q_sb + (int64_t)min(hq, a.H - 1) * a.q_sh;
+  u32x4 qrv = {0u, 0u, 0u, 0u};
+  if (wave < KR) qrv = *reinterpret_cast<const u32x4*>(qh + D + 32 * wave + 8 * gq);
+  u32x4 qv[QG][4];  // features 128g + 32gq + 8i .. +7 of group g = wave + 4 gi
+#pragma unroll
+  for (int gi = 0; gi < QG; ++gi) {
+    const int g = wave + 2 * kPairs * gi;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      qv[gi][i] = g < NG ? *reinterpret_cast<const u32x4*>(qh + 128 * g + 32 * gq + 8 * i) : u32x4{0u, 0u, 0u, 0u};
+  }
+
   // the first two tiles' loads fly while the query operands are prepared
   Pages ix0, ix1, ix2;
   if (nmine > 0) { lookup(0, ix0); dma(tile0, ix0, tb0); }
   if (nmine > 1) { lookup(1, ix1); dma(tile0 + kPairs, ix1, tb1); }
 
-  // ---- query operands (wave w prepares groups w, w + 4, .. and rope K-block w) ---
-  // s_qs[g][kbl]: lane (gq, la) = head la, element pair r of K-block kbl <->
-  // in-group features 16s+k and 16s+k+8 with s = 2gq + kbl/2, k = 4(kbl%2) + r,
-  // scaled by 2^(5-e_k). The lane reads its 32 features 32gq.. of the group
-  // with four 16-byte loads.
-  {
-    const int h = h0 + la;
-    const bool hv = h < a.H;
-    const uint16_t* qh = a.q + b * a.q_sb + (int64_t)min(h, a.H - 1) * a.q_sh;
-    if (wave < KR) {
-      // rope B operand of K-block kr: head la, dims 32kr + 8gq + i
-      const u32x4 v = *reinterpret_cast<const u32x4*>(qh + D + 32 * wave + 8 * gq);
-      s_qr[wave][lane] = hv ? v : u32x4{0, 0, 0, 0};
+  // Phase 1 forms the latent scores on MFMA with the codes as fp4 A operands
+  // (0b00cc is c/2 in e2m1: a mask, no unpacking) and the query as fp8 e4m3 B
+  // operands: q of head la scaled by 2^kq (kq per head: its largest |q| lands
+  // in [128, 256)), split into two e4m3 pieces q1 + q2. A bf16 value minus its
+  // nearest e4m3 has at most 4 significant bits, so the pair is exact for every
+  // element down to 2^-10 of the head's maximum (below, off by < 2^-10 there).
+  // A lane (token, gq) holds the codes of features 32gq .. 32gq+31 of a group:
+  // dword d nibble n = feature 32gq + 16(d>>1) + 2n + (d&1) (words 2gq, 2gq+1
+  // split into even and odd codes). With the fp4 A layout this puts feature
+  //   f(G', j) = 32 G + 16 (G'&1) + 2 (j&7) + ((j>>3)&1),  G = (G'>>1) + 2((j>>4)&1)
+  // at K = 32 G' + j, i.e. in byte j of B lane (head, G').
+  uint16_t* const qscr = reinterpret_cast<uint16_t*>(s_r2);  // [16 heads][D] bf16
+  if (wave < KR) s_qr[wave][lane] = hv ? qrv : u32x4{0, 0, 0, 0};
+#pragma unroll
+  for (int gi = 0; gi < QG; ++gi) {
+    const int g = wave + 2 * kPairs * gi;
+    if (g >= NG) break;
+    float mx = 0.f, sm = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const u32x4 v = hv ? qv[gi][i] : u32x4{0, 0, 0, 0};
+      *reinterpret_cast<u32x4*>(qscr + la * D + 128 * g + 32 * gq + 8 * i) = v;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float lo = bf16_lo(v[e]), hi = bf16_hi(v[e]);
+        mx = fmaxf(mx, fmaxf(fabsf(lo), fabsf(hi)));
+        sm += lo + hi;
+      }
     }
-    for (int g = wave; g < NG; g += 2 * kPairs) {
-      u32x4 v[4];  // features 128g + 32gq + 8i .. +7
+    mx = wave_max_over_groups(mx);
+    sm = wave_sum_over_groups(sm);
+    if (gq == 0) {
+      s_qmax[g][la] = mx;
+      s_qq[g][la].x = sm;
+    }
+  }
+  lds_barrier();
+  {
+    float hm = 0.f;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const u32x4 x = *reinterpret_cast<const u32x4*>(qh + 128 * g + 32 * gq + 8 * i);
-        v[i] = hv ? x : u32x4{0, 0, 0, 0};
+    for (int g = 0; g < NG; ++g) hm = fmaxf(hm, s_qmax[g][la]);
+    int e = 0;
+    if (hm > 0.f) frexpf(hm, &e);  // hm in [2^(e-1), 2^e)
+    const int kq = hm > 0.f ? 8 - e : 0;
+    const float qscale = ldexpf(1.f, kq);
+#pragma unroll
+    for (int gi = 0; gi < QG; ++gi) {
+      const int g = wave + 2 * kPairs * gi;
+      if (g >= NG) break;
+      uint32_t w1[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u}, w2[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
+      // bytes j and j + 8 hold adjacent features f, f + 1 (j & 8 == 0): one
+      // 32-bit read, one packed conversion per piece
+#pragma unroll
+      for (int jj = 0; jj < 16; ++jj) {
+        const int j = (jj & 7) + 16 * (jj >> 3);
+        const int G = (gq >> 1) + 2 * ((j >> 4) & 1);
+        const int f = 32 * G + 16 * (gq & 1) + 2 * (j & 7);
+        const uint32_t qw = *reinterpret_cast<const uint32_t*>(qscr + la * D + 128 * g + f);
+        const float x0 = bf16_lo(qw) * qscale, x1 = bf16_hi(qw) * qscale;
+        const uint32_t p1 = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(x0, x1, 0, false);
+        const float r0 = x0 - __builtin_amdgcn_cvt_f32_fp8((int)p1, 0);
+        const float r1 = x1 - __builtin_amdgcn_cvt_f32_fp8((int)p1, 1);
+        const uint32_t p2 = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(r0, r1, 0, false);
+        w1[j >> 2] |= (p1 & 0xffu) << (8 * (j & 3));
+        w1[(j + 8) >> 2] |= ((p1 >> 8) & 0xffu) << (8 * (j & 3));
+        w2[j >> 2] |= (p2 & 0xffu) << (8 * (j & 3));
+        w2[(j + 8) >> 2] |= ((p2 >> 8) & 0xffu) << (8 * (j & 3));
       }
-      float s_sum = 0.f, s_w = 0.f;
-#pragma unroll
-      for (int kbl = 0; kbl < 4; ++kbl) {
-        const u32x4 vlo = v[2 * (kbl / 2)], vhi = v[2 * (kbl / 2) + 1];  // k and k + 8
-        uint32_t outv[4];
-#pragma unroll
-        for (int r = 0; r < 4; ++r) {
-          const int d = 2 * (kbl % 2) + r / 2;  // dword of element 4(kbl%2) + r
-          const float vl = (r & 1) ? bf16_hi(vlo[d]) : bf16_lo(vlo[d]);
-          const float vh = (r & 1) ? bf16_hi(vhi[d]) : bf16_lo(vhi[d]);
-          const float wk = pair_weight(4 * (kbl % 2) + r);
-          s_sum += vl + vh;
-          s_w += (vl + vh) * wk;
-          outv[r] = pack_bf16(vl * wk, vh * wk);
-        }
-        s_qs[g][kbl][lane] = u32x4{outv[0], outv[1], outv[2], outv[3]};
-      }
-      s_sum = wave_sum_over_groups(s_sum);
-      s_w = wave_sum_over_groups(s_w);
-      if (gq == 0) s_qq[g][la] = f32x2{s_sum, 4.f * s_w};
+      s_qs[g][0][0][lane] = u32x4{w1[0], w1[1], w1[2], w1[3]};
+      s_qs[g][0][1][lane] = u32x4{w1[4], w1[5], w1[6], w1[7]};
+      s_qs[g][1][0][lane] = u32x4{w2[0], w2[1], w2[2], w2[3]};
+      s_qs[g][1][1][lane] = u32x4{w2[4], w2[5], w2[6], w2[7]};
+      // latent score = 2^(1-kq) sum_g scale (acc_g - zero Qsum_g 2^(kq-1))
+      if (gq == 0) s_qq[g][la] = f32x2{ldexpf(s_qq[g][la].x, kq - 1), ldexpf(1.f, 1 - kq)};
     }
   }
   lds_barrier();
@@ -484,14 +539,20 @@ __global__ __launch_bounds__(kThreads, 2) void decode_stage1(DecodeArgs a) {
   auto phase1 = [&](int tile, uint8_t* tl) {
     const int p0 = tile * TILE;
     const int tA = 16 * wh + la;  // A-operand token of this lane
-    // The query's B operands are read one group ahead of their MFMAs (group
-    // g + 1 while group g computes): read next to its MFMA, each read's LDS
-    // latency would stall the accumulation chain.
-    u32x4 qop[2][4], qrp[KR];
+    // All of the query's B operands are read up front: read next to its MFMA,
+    // each read's latency would stall the chain, and a buffer refilled while an
+    // MFMA still reads it costs wait states.
+    u32x4 qrp[KR];
+    u32x8 qop[NG][2];  // [group][piece]
 #pragma unroll
     for (int kr = 0; kr < KR; ++kr) qrp[kr] = s_qr[kr][lane];
 #pragma unroll
-    for (int kbl = 0; kbl < 4; ++kbl) qop[0][kbl] = s_qs[0][kbl][lane];
+    for (int g = 0; g < NG; ++g)
+#pragma unroll
+      for (int pc = 0; pc < 2; ++pc) {
+        const u32x4 lo4 = s_qs[g][pc][0][lane], hi4 = s_qs[g][pc][1][lane];
+        qop[g][pc] = u32x8{lo4.x, lo4.y, lo4.z, lo4.w, hi4.x, hi4.y, hi4.z, hi4.w};
+      }
     uint32_t cw[2 * NG];          // words s = 2gq (cw[g]) and 2gq+1 (cw[NG+g]) of token tA
     if constexpr (NG == 4) {
       const u32x4 v0 = lds128(tl + 16 * G::cslot(tA, 2 * gq));
@@ -503,7 +564,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_stage1(DecodeArgs a) {
       cw[0] = v0.x; cw[1] = v0.y; cw[2] = v0.z; cw[3] = v0.w;
     }
     u32x4 ropa[KR];
-    f32x2 qqv[NG];  // Qsum, 4 Q' of head la per group
+    f32x2 qqv[NG];  // Qsum 2^(kq-1), 2^(1-kq) of head la per group
 #pragma unroll
     for (int kr = 0; kr < KR; ++kr) ropa[kr] = lds128(tl + G::OFF_R + 16 * G::rslot(tA, 4 * kr + gq));
 #pragma unroll
@@ -511,38 +572,35 @@ __global__ __launch_bounds__(kThreads, 2) void decode_stage1(DecodeArgs a) {
     f32x4 accr = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int kr = 0; kr < KR; ++kr) accr = mfma16x16x32(ropa[kr], qrp[kr], accr);
-    float s[4] = {accr[0], accr[1], accr[2], accr[3]};
+    float s[4] = {0.f, 0.f, 0.f, 0.f};  // latent part, in units of 2^(1-kq)
     // C-layout tokens of this lane: 16wh + 4gq + j
+    f32x4 pv[NG / 2][4];
 #pragma unroll
-    for (int gp = 0; gp < NG / 2; ++gp) {
-      f32x4 pv[4];
+    for (int gp = 0; gp < NG / 2; ++gp)
 #pragma unroll
-      for (int j = 0; j < 4; ++j) pv[j] = lds128f(tl + G::OFF_P + (16 * wh + 4 * gq + j) * PB + 16 * gp);
+      for (int j = 0; j < 4; ++j) pv[gp][j] = lds128f(tl + G::OFF_P + (16 * wh + 4 * gq + j) * PB + 16 * gp);
+    // all groups' MFMAs (independent chains of two), then the accumulation
+    f32x4 acc[NG];
 #pragma unroll
-      for (int gg = 0; gg < 2; ++gg) {
-        const int g = 2 * gp + gg;
-        if (g + 1 < NG) {
+    for (int g = 0; g < NG; ++g) {
+      // codes as fp4: even codes of a word in one dword, odd codes in the next
+      const u32x4 a4 = {cw[g] & 0x33333333u, (cw[g] >> 2) & 0x33333333u, cw[NG + g] & 0x33333333u,
+                        (cw[NG + g] >> 2) & 0x33333333u};
+      acc[g] = mfma_f4_f8(a4, qop[g][0], f32x4{0.f, 0.f, 0.f, 0.f});
+      acc[g] = mfma_f4_f8(a4, qop[g][1], acc[g]);
+    }
 #pragma unroll
-          for (int kbl = 0; kbl < 4; ++kbl) qop[(g + 1) & 1][kbl] = s_qs[g + 1][kbl][lane];
-        }
-        __builtin_amdgcn_sched_barrier(0);
-        uint32_t d0[8], d1[8];
-        unpack_word_fast(cw[g], d0, vbase);
-        unpack_word_fast(cw[NG + g], d1, vbase);
-        const u32x4 kop[4] = {{d0[0], d0[1], d0[2], d0[3]}, {d0[4], d0[5], d0[6], d0[7]},
-                              {d1[0], d1[1], d1[2], d1[3]}, {d1[4], d1[5], d1[6], d1[7]}};
-        const f32x2 qq = qqv[g];
-        f32x4 acc = {-qq.y, -qq.y, -qq.y, -qq.y};
+    for (int g = 0; g < NG; ++g) {
+      const f32x2 qq = qqv[g];
 #pragma unroll
-        for (int kbl = 0; kbl < 4; ++kbl) acc = mfma16x16x32(kop[kbl], qop[g & 1][kbl], acc);
-#pragma unroll
-        for (int j = 0; j < 4; ++j) {
-          const float scl = gg ? pv[j].z : pv[j].x;
-          const float zr = gg ? pv[j].w : pv[j].y;
-          s[j] = fmaf(scl, fmaf(-zr, qq.x, acc[j]), s[j]);
-        }
+      for (int j = 0; j < 4; ++j) {
+        const float scl = (g & 1) ? pv[g >> 1][j].z : pv[g >> 1][j].x;
+        const float zr = (g & 1) ? pv[g >> 1][j].w : pv[g >> 1][j].y;
+        s[j] = fmaf(scl, fmaf(-zr, qq.x, acc[g][j]), s[j]);
       }
     }
+#pragma unroll
+    for (int j = 0; j < 4; ++j) s[j] = fmaf(qqv[0].y, s[j], accr[j]);
     const int pb = p0 + 16 * wh + 4 * gq;
 #pragma unroll
     for (int j = 0; j < 4; ++j) s[j] = (pb + j >= lo && pb + j < hi) ? s[j] * scale_log2 : kNoRef;
