@@ -296,7 +296,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_stage1(DecodeArgs a) {
   static_assert(R % 32 == 0 && D % 256 == 0, "unsupported shape");
   static_assert(8 * D * 4 <= RING, "merge buffer (8 heads) does not fit in one ring buffer");
   static_assert(window_half_rows_bytes<D, R>() <= RING && 4 * 16 * kMaxWindow * 4 <= RING &&
-                (16 * kMaxWindow + 16) * 4 <= NG * 4 * 64 * 16 && 16 * D * 2 <= RING, "window / query scratch");
+                (16 * kMaxWindow + 16) * 4 <= NG * 4 * 64 * 16, "window scratch");
   using Pages = TilePages<CLW, RLW, PAGED>;
 
   // Three tile buffers as separate LDS objects, so the compiler's wait
@@ -307,8 +307,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_stage1(DecodeArgs a) {
   // score-MFMA B operands of the query (fp8 e4m3): [group][piece][half][lane]
   __shared__ __attribute__((aligned(16))) u32x4 s_qs[NG][2][2][64];
   __shared__ __attribute__((aligned(16))) u32x4 s_qr[KR][64];  // rope B operands (bf16)
-  __shared__ f32x2 s_qq[NG][16];           // per group and head: Qsum 2^(kq-1), 2^(1-kq)
-  __shared__ float s_qmax[NG][16];         // per group and head: max |q|
+  __shared__ f32x2 s_qq[NG][16];           // per group and head: Qsum / 2, MFMA scale exponent (bits)
   __shared__ float s_ml[kPairs][16][2];    // per pair and head: reference max, sum
 
   const int nhg = (a.H + 15) / 16;
@@ -421,6 +420,20 @@ __global__ __launch_bounds__(kThreads, 2) void decode_stage1(DecodeArgs a) {
   uint8_t* const tb1 = s_r1 + pr * G::TILE_LDS;
   uint8_t* const tb2 = s_r2 + pr * G::TILE_LDS;
   // ---- query operands (wave w prepares groups w, w + 4, .. and rope K-block w) ---
+  // Phase 1 forms the latent scores on MFMA with the codes as fp4 A operands
+  // (0b00cc is c/2 in e2m1: a mask, no unpacking) and the query as fp8 e4m3 B
+  // operands: q of head la and group g scaled by 2^kq (its largest |q| lands in
+  // [128, 256)) and split into two e4m3 pieces q1 + q2; the MFMA's block scale
+  // 2^-kq undoes the scaling. A bf16 value minus its nearest e4m3 has at most 4
+  // significant bits, so the pair is exact for every element down to 2^-10 of
+  // the group's maximum (below, off by < 2^-10 of it).
+  // A lane (token, gq) holds the codes of features 32gq .. 32gq+31 of a group:
+  // dword d nibble n = feature 32gq + 16(d>>1) + 2n + (d&1) (words 2gq, 2gq+1
+  // split into even and odd codes). With the fp4 A layout this puts feature
+  //   f(G', j) = 32 G + 16 (G'&1) + 2 (j&7) + ((j>>3)&1),  G = (G'>>1) + 2 (j>>4)
+  // at K = 32 G' + j, byte j of B lane (head, G'): bytes j, j + 8 (j & 8 == 0)
+  // hold the adjacent features 32 G + 16 (G'&1) + 2 (j&7) + {0, 1}, so lane
+  // (head la, gq) reads its 32 features as two contiguous 16-feature chunks.
   // The query's global loads go out first, before the page lookups: they then
   // complete together with the lookups instead of queueing behind the first
   // tiles' direct loads (the memory counter drains in order).
@@ -430,13 +443,15 @@ __global__ __launch_bounds__(kThreads, 2) void decode_stage1(DecodeArgs a) {
   const uint16_t* qh = a.q + b * a.q_sb + (int64_t)min(hq, a.H - 1) * a.q_sh;
   u32x4 qrv = {0u, 0u, 0u, 0u};
   if (wave < KR) qrv = *reinterpret_cast<const u32x4*>(qh + D + 32 * wave + 8 * gq);
-  u32x4 qv[QG][4];  // features 128g + 32gq + 8i .. +7 of group g = wave + 4 gi
+  u32x4 qv[QG][4];  // chunk h (features 32((gq>>1) + 2h) + 16(gq&1) ..+15) in qv[gi][2h], [2h+1]
 #pragma unroll
   for (int gi = 0; gi < QG; ++gi) {
     const int g = wave + 2 * kPairs * gi;
 #pragma unroll
-    for (int i = 0; i < 4; ++i)
-      qv[gi][i] = g < NG ? *reinterpret_cast<const u32x4*>(qh + 128 * g + 32 * gq + 8 * i) : u32x4{0u, 0u, 0u, 0u};
+    for (int i = 0; i < 4; ++i) {
+      const int f = 32 * ((gq >> 1) + 2 * (i >> 1)) + 16 * (gq & 1) + 8 * (i & 1);
+      qv[gi][i] = g < NG ? *reinterpret_cast<const u32x4*>(qh + 128 * g + f) : u32x4{0u, 0u, 0u, 0u};
+    }
   }
 
   // the first two tiles' loads fly while the query operands are prepared
@@ -444,18 +459,6 @@ __global__ __launch_bounds__(kThreads, 2) void decode_stage1(DecodeArgs a) {
   if (nmine > 0) { lookup(0, ix0); dma(tile0, ix0, tb0); }
   if (nmine > 1) { lookup(1, ix1); dma(tile0 + kPairs, ix1, tb1); }
 
-  // Phase 1 forms the latent scores on MFMA with the codes as fp4 A operands
-  // (0b00cc is c/2 in e2m1: a mask, no unpacking) and the query as fp8 e4m3 B
-  // operands: q of head la scaled by 2^kq (kq per head: its largest |q| lands
-  // in [128, 256)), split into two e4m3 pieces q1 + q2. A bf16 value minus its
-  // nearest e4m3 has at most 4 significant bits, so the pair is exact for every
-  // element down to 2^-10 of the head's maximum (below, off by < 2^-10 there).
-  // A lane (token, gq) holds the codes of features 32gq .. 32gq+31 of a group:
-  // dword d nibble n = feature 32gq + 16(d>>1) + 2n + (d&1) (words 2gq, 2gq+1
-  // split into even and odd codes). With the fp4 A layout this puts feature
-  //   f(G', j) = 32 G + 16 (G'&1) + 2 (j&7) + ((j>>3)&1),  G = (G'>>1) + 2((j>>4)&1)
-  // at K = 32 G' + j, i.e. in byte j of B lane (head, G').
-  uint16_t* const qscr = reinterpret_cast<uint16_t*>(s_r2);  // [16 heads][D] bf16
   if (wave < KR) s_qr[wave][lane] = hv ? qrv : u32x4{0, 0, 0, 0};
 #pragma unroll
   for (int gi = 0; gi < QG; ++gi) {
@@ -464,61 +467,45 @@ __global__ __launch_bounds__(kThreads, 2) void decode_stage1(DecodeArgs a) {
     float mx = 0.f, sm = 0.f;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const u32x4 v = hv ? qv[gi][i] : u32x4{0, 0, 0, 0};
-      *reinterpret_cast<u32x4*>(qscr + la * D + 128 * g + 32 * gq + 8 * i) = v;
+      if (!hv) qv[gi][i] = u32x4{0u, 0u, 0u, 0u};
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const float lo = bf16_lo(v[e]), hi = bf16_hi(v[e]);
+        const float lo = bf16_lo(qv[gi][i][e]), hi = bf16_hi(qv[gi][i][e]);
         mx = fmaxf(mx, fmaxf(fabsf(lo), fabsf(hi)));
         sm += lo + hi;
       }
     }
-    mx = wave_max_over_groups(mx);
+    mx = wave_max_over_groups(mx);  // over the group's 128 features of head la
     sm = wave_sum_over_groups(sm);
-    if (gq == 0) {
-      s_qmax[g][la] = mx;
-      s_qq[g][la].x = sm;
-    }
-  }
-  lds_barrier();
-  {
-    float hm = 0.f;
-#pragma unroll
-    for (int g = 0; g < NG; ++g) hm = fmaxf(hm, s_qmax[g][la]);
     int e = 0;
-    if (hm > 0.f) frexpf(hm, &e);  // hm in [2^(e-1), 2^e)
-    const int kq = hm > 0.f ? 8 - e : 0;
+    if (mx > 0.f) frexpf(mx, &e);  // mx in [2^(e-1), 2^e)
+    const int kq = mx > 0.f ? 8 - e : 0;
     const float qscale = ldexpf(1.f, kq);
+    uint32_t w1[8], w2[8];
 #pragma unroll
-    for (int gi = 0; gi < QG; ++gi) {
-      const int g = wave + 2 * kPairs * gi;
-      if (g >= NG) break;
-      uint32_t w1[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u}, w2[8] = {0u, 0u, 0u, 0u, 0u, 0u, 0u, 0u};
-      // bytes j and j + 8 hold adjacent features f, f + 1 (j & 8 == 0): one
-      // 32-bit read, one packed conversion per piece
+    for (int i = 0; i < 8; ++i) w1[i] = w2[i] = 0u;
 #pragma unroll
-      for (int jj = 0; jj < 16; ++jj) {
-        const int j = (jj & 7) + 16 * (jj >> 3);
-        const int G = (gq >> 1) + 2 * ((j >> 4) & 1);
-        const int f = 32 * G + 16 * (gq & 1) + 2 * (j & 7);
-        const uint32_t qw = *reinterpret_cast<const uint32_t*>(qscr + la * D + 128 * g + f);
+    for (int h = 0; h < 2; ++h)
+#pragma unroll
+      for (int k = 0; k < 8; ++k) {  // features 2k, 2k+1 of chunk h -> bytes j = 16h + k and j + 8
+        const uint32_t qw = qv[gi][2 * h + (k >> 2)][k & 3];
         const float x0 = bf16_lo(qw) * qscale, x1 = bf16_hi(qw) * qscale;
         const uint32_t p1 = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(x0, x1, 0, false);
         const float r0 = x0 - __builtin_amdgcn_cvt_f32_fp8((int)p1, 0);
         const float r1 = x1 - __builtin_amdgcn_cvt_f32_fp8((int)p1, 1);
         const uint32_t p2 = (uint32_t)__builtin_amdgcn_cvt_pk_fp8_f32(r0, r1, 0, false);
+        const int j = 16 * h + k;
         w1[j >> 2] |= (p1 & 0xffu) << (8 * (j & 3));
         w1[(j + 8) >> 2] |= ((p1 >> 8) & 0xffu) << (8 * (j & 3));
         w2[j >> 2] |= (p2 & 0xffu) << (8 * (j & 3));
         w2[(j + 8) >> 2] |= ((p2 >> 8) & 0xffu) << (8 * (j & 3));
       }
-      s_qs[g][0][0][lane] = u32x4{w1[0], w1[1], w1[2], w1[3]};
-      s_qs[g][0][1][lane] = u32x4{w1[4], w1[5], w1[6], w1[7]};
-      s_qs[g][1][0][lane] = u32x4{w2[0], w2[1], w2[2], w2[3]};
-      s_qs[g][1][1][lane] = u32x4{w2[4], w2[5], w2[6], w2[7]};
-      // latent score = 2^(1-kq) sum_g scale (acc_g - zero Qsum_g 2^(kq-1))
-      if (gq == 0) s_qq[g][la] = f32x2{ldexpf(s_qq[g][la].x, kq - 1), ldexpf(1.f, 1 - kq)};
-    }
+    s_qs[g][0][0][lane] = u32x4{w1[0], w1[1], w1[2], w1[3]};
+    s_qs[g][0][1][lane] = u32x4{w1[4], w1[5], w1[6], w1[7]};
+    s_qs[g][1][0][lane] = u32x4{w2[0], w2[1], w2[2], w2[3]};
+    s_qs[g][1][1][lane] = u32x4{w2[4], w2[5], w2[6], w2[7]};
+    // latent score = 2 sum_g scale (A_g - zero Qsum_g / 2), A_g = sum (c / 2) q
+    if (gq == 0) s_qq[g][la] = f32x2{0.5f * sm, __int_as_float(127 - kq)};
   }
   lds_barrier();
   const uint32_t one = la == 0 ? 0x3F803F80u : 0u;
@@ -564,7 +551,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_stage1(DecodeArgs a) {
       cw[0] = v0.x; cw[1] = v0.y; cw[2] = v0.z; cw[3] = v0.w;
     }
     u32x4 ropa[KR];
-    f32x2 qqv[NG];  // Qsum 2^(kq-1), 2^(1-kq) of head la per group
+    f32x2 qqv[NG];  // Qsum / 2, MFMA scale exponent of head la per group
 #pragma unroll
     for (int kr = 0; kr < KR; ++kr) ropa[kr] = lds128(tl + G::OFF_R + 16 * G::rslot(tA, 4 * kr + gq));
 #pragma unroll
@@ -572,7 +559,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_stage1(DecodeArgs a) {
     f32x4 accr = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int kr = 0; kr < KR; ++kr) accr = mfma16x16x32(ropa[kr], qrp[kr], accr);
-    float s[4] = {0.f, 0.f, 0.f, 0.f};  // latent part, in units of 2^(1-kq)
+    float s[4] = {0.f, 0.f, 0.f, 0.f};  // latent part, halved
     // C-layout tokens of this lane: 16wh + 4gq + j
     f32x4 pv[NG / 2][4];
 #pragma unroll
@@ -586,8 +573,9 @@ __global__ __launch_bounds__(kThreads, 2) void decode_stage1(DecodeArgs a) {
       // codes as fp4: even codes of a word in one dword, odd codes in the next
       const u32x4 a4 = {cw[g] & 0x33333333u, (cw[g] >> 2) & 0x33333333u, cw[NG + g] & 0x33333333u,
                         (cw[NG + g] >> 2) & 0x33333333u};
-      acc[g] = mfma_f4_f8(a4, qop[g][0], f32x4{0.f, 0.f, 0.f, 0.f});
-      acc[g] = mfma_f4_f8(a4, qop[g][1], acc[g]);
+      const int sb = __float_as_int(qqv[g].y);  // 127 - kq of (head la, group g)
+      acc[g] = mfma_f4_f8(a4, qop[g][0], f32x4{0.f, 0.f, 0.f, 0.f}, sb);
+      acc[g] = mfma_f4_f8(a4, qop[g][1], acc[g], sb);
     }
 #pragma unroll
     for (int g = 0; g < NG; ++g) {
@@ -600,7 +588,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_stage1(DecodeArgs a) {
       }
     }
 #pragma unroll
-    for (int j = 0; j < 4; ++j) s[j] = fmaf(qqv[0].y, s[j], accr[j]);
+    for (int j = 0; j < 4; ++j) s[j] = fmaf(2.f, s[j], accr[j]);
     const int pb = p0 + 16 * wh + 4 * gq;
 #pragma unroll
     for (int j = 0; j < 4; ++j) s[j] = (pb + j >= lo && pb + j < hi) ? s[j] * scale_log2 : kNoRef;

@@ -28,20 +28,21 @@ __device__ __forceinline__ f32x4 mfma16x16x32(u32x4 a, u32x4 b, f32x4 c) {
                                                  __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
 }
 
-// D = A(16x128) * B(128x16) + C with A in fp4 (e2m1) and B in fp8 (e4m3, OCP),
-// fp32 accumulate, block scales 1 (v_mfma_scale_f32_16x16x128_f8f6f4, 32 cycles).
+// D = A(16x128) * B(128x16) 2^(sb - 127) + C with A in fp4 (e2m1) and B in fp8
+// (e4m3, OCP), fp32 accumulate (v_mfma_scale_f32_16x16x128_f8f6f4, 32 cycles).
+// sb is the E8M0 block scale of the lane's 32 K-elements of B (A's scale is 1).
 // Operand layouts (checked on the device):
 //   A lane l (row l%16, G = l/16): dword d (0..3) nibble n <-> K = 64(G&1) + 16(G>>1) + 32(d>>1) + 8(d&1) + n
 //   B lane l (col l%16, G = l/16): dword i (0..7) byte b  <-> K = 32G + 4i + b
 //   C as for mfma16x16x32.
 typedef uint32_t u32x8 __attribute__((ext_vector_type(8)));
-__device__ __forceinline__ f32x4 mfma_f4_f8(u32x4 a, u32x8 b, f32x4 c) {
+__device__ __forceinline__ f32x4 mfma_f4_f8(u32x4 a, u32x8 b, f32x4 c, int sb) {
   typedef int i32x4_t __attribute__((ext_vector_type(4)));
   typedef int i32x8_t __attribute__((ext_vector_type(8)));
   const i32x4_t a4 = __builtin_bit_cast(i32x4_t, a);
   const i32x8_t a8 = __builtin_shufflevector(a4, a4, 0, 1, 2, 3, -1, -1, -1, -1);  // fp4 uses 4 dwords
   return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a8, __builtin_bit_cast(i32x8_t, b), c, 4, 0, 0, 127, 0,
-                                                          127);
+                                                          sb);
 }
 
 // Two fp32 -> one dword of two bf16 (round to nearest even), low half = lo.
