@@ -454,10 +454,16 @@ __global__ __launch_bounds__(kThreads, 2) void decode_stage1(DecodeArgs a) {
     }
   }
 
-  // the first two tiles' loads fly while the query operands are prepared
+  // the first two tiles' loads fly while the query operands are prepared. The
+  // wait for the page lookups (which also covers the query loads) comes before
+  // the direct loads on every path: a wait for the query placed after them
+  // would also wait for the tiles.
   Pages ix0, ix1, ix2;
-  if (nmine > 0) { lookup(0, ix0); dma(tile0, ix0, tb0); }
-  if (nmine > 1) { lookup(1, ix1); dma(tile0 + kPairs, ix1, tb1); }
+  if (nmine > 0) lookup(0, ix0);
+  if (nmine > 1) lookup(1, ix1);
+  __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));
+  if (nmine > 0) dma(tile0, ix0, tb0);
+  if (nmine > 1) dma(tile0 + kPairs, ix1, tb1);
 
   if (wave < KR) s_qr[wave][lane] = hv ? qrv : u32x4{0, 0, 0, 0};
 #pragma unroll
