@@ -258,6 +258,7 @@ struct TilePages {
   int cs[PAGED ? 1 : CLW], rs[PAGED ? 1 : RLW], ps;
 };
 
+constexpr int kXcds = 8;                 // accelerator dies (own L2 each) of the MI355X
 constexpr int kPairs = 2;                // wave pairs per block
 constexpr int kThreads = 128 * kPairs;   // 4 waves; two blocks share a CU
 constexpr float kNoRef = -1.0e30f;       // "no score yet" / masked score (log2 units)
@@ -311,7 +312,18 @@ __global__ __launch_bounds__(kThreads, 2) void decode_stage1(DecodeArgs a) {
   __shared__ float s_ml[kPairs][16][2];    // per pair and head: reference max, sum
 
   const int nhg = (a.H + 15) / 16;
-  const int b = blockIdx.x / nhg, h0 = 16 * (blockIdx.x % nhg), split = blockIdx.y;
+  // Head groups of one (sequence, split) read the same cache rows. With more
+  // than one, the blocks are renumbered so that the nhg blocks of a (sequence,
+  // split) get consecutive dispatch slots of one XCD (the dispatcher deals
+  // linear block ids to the 8 XCDs round-robin): the second and later read the
+  // rows from that XCD's L2 instead of HBM.
+  int lin = blockIdx.x + gridDim.x * blockIdx.y;
+  const int nblk = gridDim.x * gridDim.y;
+  if (nhg > 1 && nblk % kXcds == 0) lin = (lin % kXcds) * (nblk / kXcds) + lin / kXcds;
+  const int hg = lin % nhg, rest = lin / nhg;
+  const int split = nhg > 1 ? rest % gridDim.y : blockIdx.y;
+  const int b = nhg > 1 ? rest / gridDim.y : blockIdx.x / nhg;
+  const int h0 = 16 * (nhg > 1 ? hg : blockIdx.x % nhg);
   const int ns = a.num_kv_splits[b];
   const int nq = min(max(ns - 1, 1), a.S1 - 1);
   if (split > nq) return;
