@@ -39,9 +39,8 @@ struct ExtGeo {
   static constexpr int BM = 4 * RW;                 // query rows per block
   static constexpr int ND = D / 16;                 // output column blocks
   static constexpr int KSTR = 2 * DR + 16;          // bytes per key row in LDS
-  static constexpr int VSTR = 2 * kExtKeys + 16;    // bytes per latent column in LDS
   static constexpr int KBYTES = kExtKeys * KSTR;
-  static constexpr int BUF = KBYTES + D * VSTR;     // one tile
+  static constexpr int BUF = KBYTES;                // one tile: key rows only
   static constexpr int OPT = D / 256;               // latent octets per loader thread
 };
 
@@ -137,22 +136,19 @@ __device__ __forceinline__ void load_tile(const ExtendArgs& a, TileRaw<D, R>& t,
   }
 }
 
-// Dequantize (INT2 rows) and store one tile: key rows for the scores, the
-// latent transposed for the output (keys of a column in the order the score
-// MFMA leaves them in its lanes: position 8 gq + j holds key tau(gq, j)).
+// Dequantize (INT2 rows) and store one tile's key rows [key][latent | rope]
+// (bf16). The output MFMA reads the latent transposed out of the same rows.
 template <int D, int R>
 __device__ __forceinline__ void store_tile(const TileRaw<D, R>& t, uint8_t* buf, int kq, int o) {
   using G = ExtGeo<D, R>;
   constexpr int OPT = G::OPT;
   uint8_t* kb = buf;
-  uint8_t* vb = buf + G::KBYTES;
-  const int vpos = 2 * (8 * (kq & 3) + 4 * (kq >> 2));
 #pragma unroll
   for (int j = 0; j < OPT; ++j) {
-    u32x4 v[4];
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       const uint32_t m = (t.mode >> (2 * k)) & 3u;
+      u32x4 v;
       if (m == 2u) {
         // (code - zero) * scale, rounded to bf16 as the reference's QDQ rows are
         const uint32_t bits = OPT == 2 ? (t.code[k] >> (16 * j)) : t.code[k];
@@ -160,23 +156,11 @@ __device__ __forceinline__ void store_tile(const TileRaw<D, R>& t, uint8_t* buf,
         float f[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) f[e] = (float((bits >> (2 * e)) & 3u) - z) * sc;
-        v[k] = u32x4{pack_bf16(f[0], f[1]), pack_bf16(f[2], f[3]), pack_bf16(f[4], f[5]), pack_bf16(f[6], f[7])};
+        v = u32x4{pack_bf16(f[0], f[1]), pack_bf16(f[2], f[3]), pack_bf16(f[4], f[5]), pack_bf16(f[6], f[7])};
       } else {
-        v[k] = t.lat[k][j];
+        v = t.lat[k][j];
       }
-      *reinterpret_cast<u32x4*>(kb + (4 * kq + k) * G::KSTR + 16 * (OPT * o + j)) = v[k];
-    }
-    // transpose 4 keys x 8 columns -> 8 columns x 4 keys
-    const int d0 = 8 * (OPT * o + j);
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      // columns d0 + 2e (low halves) and d0 + 2e + 1 (high halves)
-      const uint32_t lo01 = __builtin_amdgcn_perm(v[1][e], v[0][e], 0x05040100u);
-      const uint32_t lo23 = __builtin_amdgcn_perm(v[3][e], v[2][e], 0x05040100u);
-      const uint32_t hi01 = __builtin_amdgcn_perm(v[1][e], v[0][e], 0x07060302u);
-      const uint32_t hi23 = __builtin_amdgcn_perm(v[3][e], v[2][e], 0x07060302u);
-      *reinterpret_cast<u32x2*>(vb + (d0 + 2 * e) * G::VSTR + vpos) = u32x2{lo01, lo23};
-      *reinterpret_cast<u32x2*>(vb + (d0 + 2 * e + 1) * G::VSTR + vpos) = u32x2{hi01, hi23};
+      *reinterpret_cast<u32x4*>(kb + (4 * kq + k) * G::KSTR + 16 * (OPT * o + j)) = v;
     }
   }
   if (o < R / 8) {
@@ -184,6 +168,21 @@ __device__ __forceinline__ void store_tile(const TileRaw<D, R>& t, uint8_t* buf,
     for (int k = 0; k < 4; ++k)
       *reinterpret_cast<u32x4*>(kb + (4 * kq + k) * G::KSTR + 2 * D + 16 * o) = t.rope[k];
   }
+}
+
+// 64 bits of the output MFMA's B operand, read transposed out of the key rows
+// (ds_read_b64_tr_b16: within each 16-lane group, lane 4s + e receives element
+// e of the chunks addressed by lanes s, s + 4, s + 8, s + 12). Lane (gq, la)
+// addresses key row tau(gq, 4h + (la >> 2)) at latent columns 16 nd + 4 (la & 3),
+// so it receives rows tau(gq, 4h + 0..3) of column 16 nd + la: K-index
+// 8 gq + 4h + k of B is key tau(gq, 4h + k), the order P is held in.
+__device__ __forceinline__ u32x2 read_v_tr(const uint8_t* kb, int kstr, int gq, int la, int nd, int h) {
+  typedef short s16x4 __attribute__((ext_vector_type(4)));
+  const int key = 16 * h + 4 * gq + (la >> 2);
+  const uint8_t* p = kb + key * kstr + 2 * (16 * nd + 4 * (la & 3));
+  typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+  const s16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p));
+  return __builtin_bit_cast(u32x2, v);
 }
 
 template <int D, int R>
@@ -255,7 +254,6 @@ __global__ __launch_bounds__(256, 1) void extend_kernel(ExtendArgs a) {
 
     for (int it = 0; it < ntiles; ++it) {
       const uint8_t* kb = s_buf + (it & 1) * G::BUF;
-      const uint8_t* vb = kb + G::KBYTES;
       const int k0 = it * kExtKeys;
       // loads of the next tile first: they have this tile's compute to land
       // (its pages were looked up an iteration ago)
@@ -329,7 +327,8 @@ __global__ __launch_bounds__(256, 1) void extend_kernel(ExtendArgs a) {
       // ---- O[row, d] += P . V ------------------------------------------------
 #pragma unroll
       for (int nd = 0; nd < ND; ++nd) {
-        const u32x4 vf = *reinterpret_cast<const u32x4*>(vb + (16 * nd + la) * G::VSTR + 16 * gq);
+        const u32x2 v0 = read_v_tr(kb, G::KSTR, gq, la, nd, 0), v1 = read_v_tr(kb, G::KSTR, gq, la, nd, 1);
+        const u32x4 vf = {v0.x, v0.y, v1.x, v1.y};
 #pragma unroll
         for (int nb = 0; nb < NBR; ++nb) {
           acc_o[nb][nd] = mfma16x16x32(pf[nb], vf, acc_o[nb][nd]);
