@@ -83,13 +83,30 @@ __device__ __forceinline__ void lookup_tile(const ExtendArgs& a, int32_t pg[4], 
   }
 }
 
-template <int D, int R>
+// INT2 = true: every key of the tile is an INT2 prefix row (the tile lies in
+// [P, min(prefix, L - W))), so no per-key source selection is needed.
+template <int D, int R, bool INT2>
 __device__ __forceinline__ void load_tile(const ExtendArgs& a, TileRaw<D, R>& t, const int32_t pg[4], int k0,
                                           int kq, int o, int64_t qo0, int64_t prefix, int64_t L, int64_t req,
                                           int kend) {
   constexpr int NG = D / 128, OPT = ExtGeo<D, R>::OPT;
   const int dlo = 8 * OPT * o;  // first latent column of this thread
   const int g = dlo / 128, e0 = dlo % 128;
+  if constexpr (INT2) {
+    const uint32_t coff = 4 * (NG * (e0 / 16) + g) + (OPT == 2 ? 0 : 2 * ((e0 / 8) & 1));
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int kp = k0 + 4 * kq + k;
+      const uint32_t slot = ((uint32_t)pg[k] << a.page_shift) + (kp & ((1 << a.page_shift) - 1));
+      const uint64_t sl = slot;  // 64-bit offsets: a pool may exceed 4 GB per array
+      if constexpr (OPT == 2) t.code[k] = gload<uint32_t>(a.codes + sl * (D / 4) + coff);
+      else t.code[k] = gload<uint16_t>(a.codes + sl * (D / 4) + coff);
+      t.prm[k] = gload<f32x2>(a.params + sl * (2 * NG) + 2 * g);
+      t.rope[k] = o < R / 8 ? gload<u32x4>(a.rope + sl * R + 8 * o) : u32x4{0u, 0u, 0u, 0u};
+    }
+    t.mode = 0xAAu;
+    return;
+  }
   // where each key's bytes are (all addresses first: the pages were loaded an
   // iteration ago, and no load below may wait behind another)
   const uint16_t* lat[4];
@@ -138,7 +155,7 @@ __device__ __forceinline__ void load_tile(const ExtendArgs& a, TileRaw<D, R>& t,
 
 // Dequantize (INT2 rows) and store one tile's key rows [key][latent | rope]
 // (bf16). The output MFMA reads the latent transposed out of the same rows.
-template <int D, int R>
+template <int D, int R, bool INT2>
 __device__ __forceinline__ void store_tile(const TileRaw<D, R>& t, uint8_t* buf, int kq, int o) {
   using G = ExtGeo<D, R>;
   constexpr int OPT = G::OPT;
@@ -149,7 +166,7 @@ __device__ __forceinline__ void store_tile(const TileRaw<D, R>& t, uint8_t* buf,
     for (int k = 0; k < 4; ++k) {
       const uint32_t m = (t.mode >> (2 * k)) & 3u;
       u32x4 v;
-      if (m == 2u) {
+      if (INT2 || m == 2u) {
         // (code - zero) * scale, rounded to bf16 as the reference's QDQ rows are
         const uint32_t bits = OPT == 2 ? (t.code[k] >> (16 * j)) : t.code[k];
         const float sc = t.prm[k].x, z = t.prm[k].y;
@@ -232,6 +249,10 @@ __global__ __launch_bounds__(256, 1) void extend_kernel(ExtendArgs a) {
 #pragma unroll
   for (int nb = 0; nb < NBR; ++nb) qp[nb] = (int)qpos[nb];
 
+  // a tile of INT2 prefix rows only ([P, min(prefix, L - W))): loads without per-key selection
+  const int64_t int2_end = min(prefix, L - (int64_t)a.W);
+  auto int2_tile = [&](int t0) { return t0 >= a.P && (int64_t)t0 + kExtKeys <= int2_end; };
+
   f32x4 acc_o[NBR][ND];
   float m_ref[NBR], m_lane[NBR], l_run[NBR];
   bool redo = false;
@@ -247,9 +268,9 @@ __global__ __launch_bounds__(256, 1) void extend_kernel(ExtendArgs a) {
     TileRaw<D, R> raw;
     int32_t sl[4];
     lookup_tile<D, R>(a, sl, 0, kq, prefix, kv0, kend);
-    load_tile<D, R>(a, raw, sl, 0, kq, o, qo0, prefix, L, req, kend);
+    load_tile<D, R, false>(a, raw, sl, 0, kq, o, qo0, prefix, L, req, kend);
     lookup_tile<D, R>(a, sl, kExtKeys, kq, prefix, kv0, kend);
-    store_tile<D, R>(raw, s_buf, kq, o);
+    store_tile<D, R, false>(raw, s_buf, kq, o);
     __syncthreads();
 
     for (int it = 0; it < ntiles; ++it) {
@@ -258,7 +279,8 @@ __global__ __launch_bounds__(256, 1) void extend_kernel(ExtendArgs a) {
       // loads of the next tile first: they have this tile's compute to land
       // (its pages were looked up an iteration ago)
       if (it + 1 < ntiles) {
-        load_tile<D, R>(a, raw, sl, k0 + kExtKeys, kq, o, qo0, prefix, L, req, kend);
+        if (int2_tile(k0 + kExtKeys)) load_tile<D, R, true>(a, raw, sl, k0 + kExtKeys, kq, o, qo0, prefix, L, req, kend);
+        else load_tile<D, R, false>(a, raw, sl, k0 + kExtKeys, kq, o, qo0, prefix, L, req, kend);
         lookup_tile<D, R>(a, sl, k0 + 2 * kExtKeys, kq, prefix, kv0, kend);
       }
 
@@ -337,7 +359,10 @@ __global__ __launch_bounds__(256, 1) void extend_kernel(ExtendArgs a) {
       }
 
       // ---- next tile into the other buffer (last read before the previous barrier)
-      if (it + 1 < ntiles) store_tile<D, R>(raw, s_buf + ((it + 1) & 1) * G::BUF, kq, o);
+      if (it + 1 < ntiles) {
+        if (int2_tile(k0 + kExtKeys)) store_tile<D, R, true>(raw, s_buf + ((it + 1) & 1) * G::BUF, kq, o);
+        else store_tile<D, R, false>(raw, s_buf + ((it + 1) & 1) * G::BUF, kq, o);
+      }
       __syncthreads();
     }
 
