@@ -778,14 +778,20 @@ __global__ __launch_bounds__(kThreads, 2) void decode_stage1(DecodeArgs a) {
       for (int j = 0; j < 4; ++j) O[gg][nbl][j] = ((O[gg][nbl][j] - 4.f * spo[j]) * wgt - zpo[j]) * fac[j];
     }
   }
-  // pair 1 hands its partials to pair 0 through LDS in the accumulator layout
-  // (wave wh of the pair through buffer wh): plain stores and loads, no
-  // read-modify-write chains; pair 0 adds them (p0 + p1, a fixed order)
-  static_assert(kPairs == 2, "the merge below is written for two pairs");
-  static_assert(GW * 8 * 64 * 16 <= RING, "partial buffer");
-  f32x4* xb = reinterpret_cast<f32x4*>(wh == 0 ? s_r0 : s_r1);
+  // pairs 1 .. kPairs-1 hand their partials to pair 0 through LDS in the
+  // accumulator layout (plain stores and loads, no read-modify-write chains);
+  // pair 0 adds them in a fixed order (p0 + p1 + p2 + ..). Wave wh of pair pr
+  // uses partial slot 2 (pr - 1) + wh: two per ring buffer when they fit.
+  constexpr int PBUF = GW * 8 * 64 * 16;                   // bytes of one wave's partial
+  constexpr int PER_RING = 2 * PBUF <= RING ? 2 : 1;
+  static_assert(PBUF <= RING && 2 * (kPairs - 1) <= 3 * PER_RING, "partial buffers");
+  auto pslot = [&](int q) {
+    uint8_t* ring = (q / PER_RING) == 0 ? s_r0 : (q / PER_RING) == 1 ? s_r1 : s_r2;
+    return reinterpret_cast<f32x4*>(ring + (q % PER_RING) * PBUF);
+  };
   auto slot4 = [&](int gg, int nbl) { return (gg * 8 + nbl) * 64 + lane; };
-  if (pr == 1) {
+  if (pr > 0) {
+    f32x4* xb = pslot(2 * (pr - 1) + wh);
 #pragma unroll
     for (int gg = 0; gg < GW; ++gg)
 #pragma unroll
@@ -794,9 +800,13 @@ __global__ __launch_bounds__(kThreads, 2) void decode_stage1(DecodeArgs a) {
   __syncthreads();
   if (pr == 0) {
 #pragma unroll
-    for (int gg = 0; gg < GW; ++gg)
+    for (int p = 1; p < kPairs; ++p) {
+      const f32x4* xb = pslot(2 * (p - 1) + wh);
 #pragma unroll
-      for (int nbl = 0; nbl < 8; ++nbl) O[gg][nbl] += xb[slot4(gg, nbl)];
+      for (int gg = 0; gg < GW; ++gg)
+#pragma unroll
+        for (int nbl = 0; nbl < 8; ++nbl) O[gg][nbl] += xb[slot4(gg, nbl)];
+    }
   }
   __syncthreads();  // partials consumed: s_r2 / s_r0 take heads 0-7 / 8-15
   auto obuf = [&](int h) { return reinterpret_cast<float*>(h < 8 ? s_r2 : s_r0) + (h & 7) * D; };
