@@ -1,0 +1,76 @@
+"""GPU quantize-dequantize of latent rows (the HF fake-quantized cache path).
+
+``rotate_quantize`` mirrors mla_quant/quantizer.py:102-124 (name, arguments,
+cast order): rotate in FP32 with ``R_eff = fp32(bf16(R))``, Lloyd INT2 QDQ per
+group of 128, round to the input dtype, rotate back in FP32 and round again;
+rows flagged in ``high_precision_mask`` come back untouched. The reference's
+``FakeQuantizedDynamicCache`` (mla_quant/cache.py:683-1118) applies it to every
+cached latent row on update; here it runs as two launches of this library's
+kernels instead of torch CPU/GPU ops:
+
+1. the fused writer (rotation on bf16 MFMA with FP32 accumulation -- both
+   operands are bf16-exact -- then the quantizer) into scratch codes/params;
+2. the dequantize-rows kernel with un-rotation: ``(code - zero) * scale``
+   rounded to bf16, times ``R_eff^T`` in FP32, rounded to bf16.
+
+Only the summation order differs from the reference, so codes agree except for
+rare +-1 flips at rounding boundaries (the writer's parity bar).
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import kernels
+from .writer import LM_GAIN, LM_THRESHOLD, SUPPORTED_DIMS
+
+GROUP_SIZE = 128
+
+
+def rotate_quantize(latent: torch.Tensor, rotation: torch.Tensor, threshold: float = LM_THRESHOLD,
+                    gain: float = LM_GAIN, high_precision_mask: torch.Tensor | None = None,
+                    group_size: int = GROUP_SIZE) -> torch.Tensor:
+    """Restored bf16 ``latent`` (any leading shape, last dim D) after rotate -> QDQ -> un-rotate.
+
+    ``latent`` must be bf16 on the GPU and ``rotation`` a ``[D, D]`` FP32
+    matrix; ``threshold``/``gain`` are the layer's Lloyd parameters.
+    """
+    if group_size != GROUP_SIZE:
+        raise ValueError("the packed INT2 path quantizes groups of 128")
+    if latent.dtype != torch.bfloat16 or not latent.is_cuda:
+        raise ValueError("latent must be a bf16 GPU tensor")
+    D = latent.shape[-1]
+    R = 16 * (D // GROUP_SIZE)  # rope width the kernels are built for at this D
+    if (D, R) not in SUPPORTED_DIMS:
+        raise ValueError(f"unsupported latent width {D}")
+    if rotation.dtype != torch.float32 or tuple(rotation.shape) != (D, D):
+        raise ValueError("rotation must be a [D, D] FP32 matrix")
+    mask = None
+    if high_precision_mask is not None:
+        mask = torch.broadcast_to(high_precision_mask.to(device=latent.device, dtype=torch.bool), latent.shape[:-1])
+        if bool(mask.all()):
+            return latent
+    dev = latent.device
+    x = latent.reshape(-1, D).contiguous()
+    n = x.shape[0]
+    if n == 0:
+        return latent.clone()
+    r_eff = rotation.to(device=dev, dtype=torch.bfloat16)
+    # scratch cache: slots 1..n (slot 0 is the padding slot), no BF16 window
+    codes = torch.empty(n + 1, D // 4, dtype=torch.uint8, device=dev)
+    params = torch.empty(n + 1, D // GROUP_SIZE, 2, dtype=torch.float32, device=dev)
+    rope = torch.empty(n + 1, R, dtype=torch.bfloat16, device=dev)
+    hp = torch.empty(1, D, dtype=torch.bfloat16, device=dev)
+    row = torch.full((n + 1,), -1, dtype=torch.int32, device=dev)
+    owner = torch.zeros(1, dtype=torch.int32, device=dev)
+    slots = torch.arange(1, n + 1, dtype=torch.int64, device=dev)
+    ones = torch.ones(n, dtype=torch.int64, device=dev)
+    kernels.write_rows(x, torch.zeros(n, R, dtype=torch.bfloat16, device=dev), r_eff.t().contiguous(), slots, ones,
+                       None, torch.zeros(n, dtype=torch.int64, device=dev), codes, params, rope, hp, row, owner,
+                       0, 0, 1, float(threshold), float(gain))
+    out = torch.empty(n, D + R, dtype=torch.bfloat16, device=dev)
+    kernels.assemble_rows(slots, codes, params, rope, hp, row, owner, r_eff.contiguous(), out)
+    restored = out[:, :D].reshape(latent.shape)
+    if mask is None:
+        return restored
+    return torch.where(mask.unsqueeze(-1), latent, restored)
