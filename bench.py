@@ -422,6 +422,22 @@ def reported_decode_result(args, dev: str, name: str) -> dict:
     return res
 
 
+def qdq_result(args, dev: str) -> dict:
+    """GPU rotate_quantize (the fake-quantized cache path) on 32 x 4096 rows of D = 512."""
+    from mla_kv_quant_amd import qdq, synth
+
+    n, D = 32 * 4096, 512
+    x = synth.make_latent(n, D, 5, seed=70_000, device=dev).reshape(32, 4096, D)
+    rot = synth.make_rotation(D, 70)
+    ms = time_loop(lambda: qdq.rotate_quantize(x, rot), max(5, args.steps // 2), args.warmup)
+    res = {"workload": "rotate_quantize (QDQ) of 32 x 4096 latent rows, D=512, two launches + scratch",
+           "rows": n, "us": round(ms * 1000, 2), "mrows_per_s": round(n / (ms * 1e-3) / 1e6, 1)}
+    print(f"[bench] qdq: {ms * 1000:.1f} us for {n} rows", file=sys.stderr, flush=True)
+    del x
+    torch.cuda.empty_cache()
+    return res
+
+
 def writer_result(args, dev: str) -> dict:
     wb = WriterBench(args.layers, dev)
     wms = time_loop(wb.step, max(3, args.steps // 2), args.warmup)
@@ -465,7 +481,9 @@ def main():
         print(json.dumps(extend_result(args, dev)), flush=True)
         return
     if args.reported_only:
-        print(json.dumps({k: reported_decode_result(args, dev, k) for k in ("cfg3", "cfg4a")}), flush=True)
+        out = {k: reported_decode_result(args, dev, k) for k in ("cfg3", "cfg4a")}
+        out["qdq"] = qdq_result(args, dev)
+        print(json.dumps(out), flush=True)
         return
     t_setup = time.time()
     db = DecodeBench(args.layers, dev)
@@ -519,6 +537,7 @@ def main():
         result["extend"] = extend_result(args, dev)
     if not args.no_reported:
         result["reported"] = {k: reported_decode_result(args, dev, k) for k in ("cfg3", "cfg4a")}
+        result["reported"]["qdq"] = qdq_result(args, dev)
     if not args.no_cpu:
         if not hasattr(db, "caches"):
             db = DecodeBench(1, dev)
