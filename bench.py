@@ -237,6 +237,21 @@ class WriterBench:
                                d["codes"], d["params"], d["rope"], d["hp"], d["row"], d["owner"],
                                self.P, self.W, self.max_reqs, synth.DEFAULT_THRESHOLD, synth.DEFAULT_GAIN)
 
+    def norm_step(self, rows_out: bool = True):
+        """The same writes with kv_a_layernorm fused in front (x read as the
+        pre-norm kv_a); with ``rows_out`` the normalized rows are also stored
+        to ``y`` (the MHA prefill path's kv_b_proj input)."""
+        from mla_kv_quant_amd import kernels, synth
+
+        if not hasattr(self, "gamma"):
+            self.gamma = synth.make_norm_weight(self.D, 7, device=self.dev)
+            self.y = torch.empty(self.n, self.D, dtype=torch.bfloat16, device=self.dev)
+        for d in self.layers_data:
+            kernels.norm_write_rows(d["x"], self.gamma, 1e-6, self.y if rows_out else None, d["pe"], d["rt"], self.loc, self.seqs,
+                                    self.positions, self.reqs, d["codes"], d["params"], d["rope"], d["hp"], d["row"],
+                                    d["owner"], self.P, self.W, self.max_reqs, synth.DEFAULT_THRESHOLD,
+                                    synth.DEFAULT_GAIN)
+
     def bytes_per_layer(self) -> float:
         D, R, n = self.D, self.R, self.n
         kept = self.SEQS * (self.P + self.W)
@@ -451,7 +466,12 @@ def writer_result(args, dev: str) -> dict:
         "hbm_frac": round(wach / HBM_PEAK_GBS, 4),
         "mfma_frac": round(wb.flops_per_layer() / (wus * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
     }
-    print(f"[bench] writer: {wus:.2f} us/layer, {res['mtokens_per_s']} Mtok/s", file=sys.stderr, flush=True)
+    for key, rows_out in (("norm_fused_us_per_layer", False), ("norm_fused_rows_out_us_per_layer", True)):
+        nms = time_loop(lambda: wb.norm_step(rows_out), max(3, args.steps // 2), args.warmup)
+        res[key] = round(nms * 1000.0 / args.layers, 3)
+    print(f"[bench] writer: {wus:.2f} us/layer, {res['mtokens_per_s']} Mtok/s; with kv_a_layernorm fused: "
+          f"{res['norm_fused_us_per_layer']} us/layer, and the normalized rows stored: "
+          f"{res['norm_fused_rows_out_us_per_layer']} us/layer", file=sys.stderr, flush=True)
     del wb
     torch.cuda.empty_cache()
     return res

@@ -83,6 +83,30 @@ int rolaq_write_rows(const void* latent, int64_t latent_stride, const void* k_pe
                      void* hp_c, int32_t* row_of_slot, int32_t* owner_of_row, void* stream);
 
 /*
+ * kv_a_layernorm fused in front of the writer: every row of kv_a (the
+ * pre-norm compressed latent, bf16 [n, D], row stride kv_a_stride) becomes
+ *   c = bf16(norm_weight * bf16(x * rsqrt(mean(x^2) + eps)))
+ * (FP32 statistics) and is then rotated, quantized and stored exactly as
+ * rolaq_write_rows stores c. latent_out (bf16 [n, D], row stride
+ * latent_out_stride) receives c when not NULL (the un-rotated latent that
+ * an MHA prefill feeds to kv_b_proj). norm_weight: bf16 [D]. rotation_t is
+ * required (pass the identity for an un-rotated layer: the products stay exact).
+ * Replaces: self.kv_a_layernorm(kv_a) followed by try_fast_decode_store
+ *   (norm: DeepseekV2RMSNorm.forward, transformers
+ *   models/deepseek_v2/modeling_deepseek_v2.py:166-171, whose output the
+ *   reference's quantizer hooks, mla_quant/objectives.py:25-29 and
+ *   mla_quant/calibrate.py:40; writer as rolaq_write_rows).
+ */
+int rolaq_norm_write_rows(const void* kv_a, int64_t kv_a_stride, const void* norm_weight, float eps,
+                          void* latent_out, int64_t latent_out_stride, const void* k_pe,
+                          int64_t pe_stride0, int64_t pe_stride1, const void* rotation_t,
+                          const int64_t* loc, const int64_t* seq_lens, const int64_t* positions,
+                          const int64_t* req_idx, int64_t n, int D, int R, int P, int W,
+                          int max_reqs, float threshold, double gain, uint8_t* codes, float* params,
+                          void* rope_buf, void* hp_c, int32_t* row_of_slot, int32_t* owner_of_row,
+                          void* stream);
+
+/*
  * quant[i] = max(splits[i] - 1, 1); merge[i] = quant[i] + 1 (one launch).
  * Replaces: prepare_gf_splits(splits, quant, merge)
  *   (deployment/patches/rolaq_sglang.patch:81-92). int32 [n] each.

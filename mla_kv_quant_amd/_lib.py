@@ -25,6 +25,10 @@ SIGNATURES = {
                          c_void_p, c_void_p, c_int64, c_int, c_int, c_int, c_int, c_int, c_float,
                          c_double, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                          c_void_p],
+    "rolaq_norm_write_rows": [c_void_p, c_int64, c_void_p, c_float, c_void_p, c_int64, c_void_p, c_int64,
+                              c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_int, c_int,
+                              c_int, c_int, c_int, c_float, c_double, c_void_p, c_void_p, c_void_p, c_void_p,
+                              c_void_p, c_void_p, c_void_p],
     "rolaq_prepare_gf_splits": [c_void_p, c_void_p, c_void_p, c_int64, c_void_p],
     "rolaq_decode_fwd": [c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                          c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int,

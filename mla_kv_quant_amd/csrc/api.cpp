@@ -83,35 +83,38 @@ int rolaq_scatter_pack_rows(const float* x, int64_t x_stride, const int32_t* slo
                     "scatter_pack_rows launch");
 }
 
-int rolaq_write_rows(const void* latent, int64_t latent_stride, const void* k_pe, int64_t pe_stride0,
-                     int64_t pe_stride1, const void* rotation_t, const int64_t* loc, const int64_t* seq_lens,
-                     const int64_t* positions, const int64_t* req_idx, int64_t n, int D, int R, int P, int W,
-                     int max_reqs, float threshold, double gain, uint8_t* codes, float* params, void* rope_buf,
-                     void* hp_c, int32_t* row_of_slot, int32_t* owner_of_row, void* stream) {
-  if (n < 0) return fail(ROLAQ_ERR_INVALID, "write_rows: n < 0");
-  if (n == 0) { g_err[0] = '\0'; return ROLAQ_OK; }
+}  // extern "C"
+
+namespace {
+
+// Checks shared by the writer entry points; returns ROLAQ_OK or the failure.
+int check_writer(const char* fn, const void* latent, int64_t latent_stride, const void* k_pe,
+                 const void* rotation_t, const int64_t* loc, const int64_t* seq_lens, const int64_t* req_idx,
+                 int D, int R, int P, int W, int max_reqs, float threshold, double gain, const uint8_t* codes,
+                 const float* params, const void* rope_buf, const void* hp_c, const int32_t* row_of_slot,
+                 const int32_t* owner_of_row) {
   if (!((D == 512 && R == 64) || (D == 256 && R == 32)))
-    return fail(ROLAQ_ERR_INVALID, "write_rows: (D, R) must be (512, 64) or (256, 32), got (%d, %d)", D, R);
+    return fail(ROLAQ_ERR_INVALID, "%s: (D, R) must be (512, 64) or (256, 32), got (%d, %d)", fn, D, R);
   if (!latent || !k_pe || !loc || !seq_lens || !req_idx || !codes || !params || !rope_buf || !hp_c ||
       !row_of_slot || !owner_of_row)
-    return fail(ROLAQ_ERR_INVALID, "write_rows: null pointer");
-  if (latent_stride < D || latent_stride % 8 || !aligned(latent, 16))
-    return fail(ROLAQ_ERR_INVALID, "write_rows: latent must be 16-byte aligned with a row stride >= D, multiple of 8");
-  if (rotation_t && !aligned(rotation_t, 16)) return fail(ROLAQ_ERR_INVALID, "write_rows: rotation must be 16-byte aligned");
-  if (P < 0 || W < 0 || max_reqs < 0) return fail(ROLAQ_ERR_INVALID, "write_rows: negative window or max_reqs");
-  if (!good_params(threshold, gain)) return fail(ROLAQ_ERR_INVALID, "write_rows: invalid threshold/gain");
+    return fail(ROLAQ_ERR_INVALID, "%s: null pointer", fn);
+  if (latent_stride < D || latent_stride % 8 || latent_stride >= (1 << 24) || !aligned(latent, 16))
+    return fail(ROLAQ_ERR_INVALID,
+                "%s: latent must be 16-byte aligned with a row stride >= D, multiple of 8, below 2^24", fn);
+  if (rotation_t && !aligned(rotation_t, 16)) return fail(ROLAQ_ERR_INVALID, "%s: rotation must be 16-byte aligned", fn);
+  if (P < 0 || W < 0 || max_reqs < 0) return fail(ROLAQ_ERR_INVALID, "%s: negative window or max_reqs", fn);
+  if (!good_params(threshold, gain)) return fail(ROLAQ_ERR_INVALID, "%s: invalid threshold/gain", fn);
   if (!aligned(codes, 4) || !aligned(params, 8) || !aligned(hp_c, 8))
-    return fail(ROLAQ_ERR_INVALID, "write_rows: misaligned cache buffers");
-  const float ks = lloyd_kscale(gain);
-  hipStream_t s = static_cast<hipStream_t>(stream);
-  if (!rotation_t) {
-    rolaq::AuxArgs aux{static_cast<const uint16_t*>(k_pe), pe_stride0, pe_stride1, seq_lens, positions, req_idx,
-                       R, P, W, max_reqs, static_cast<uint16_t*>(rope_buf), static_cast<uint16_t*>(hp_c),
-                       row_of_slot, owner_of_row};
-    return hip_status(rolaq_launch_pack_bf16_aux(static_cast<const uint16_t*>(latent), latent_stride, loc, n, D,
-                                                 threshold, ks, codes, params, aux, s),
-                      "write_rows (un-rotated) launch");
-  }
+    return fail(ROLAQ_ERR_INVALID, "%s: misaligned cache buffers", fn);
+  return ROLAQ_OK;
+}
+
+rolaq::WriterArgs writer_args(const void* latent, int64_t latent_stride, const void* k_pe, int64_t pe_stride0,
+                              int64_t pe_stride1, const void* rotation_t, const int64_t* loc,
+                              const int64_t* seq_lens, const int64_t* positions, const int64_t* req_idx,
+                              int64_t n, int R, int P, int W, int max_reqs, float threshold, double gain,
+                              uint8_t* codes, float* params, void* rope_buf, void* hp_c, int32_t* row_of_slot,
+                              int32_t* owner_of_row) {
   rolaq::WriterArgs a{};
   a.x = static_cast<const uint16_t*>(latent);
   a.xs = latent_stride;
@@ -119,7 +122,7 @@ int rolaq_write_rows(const void* latent, int64_t latent_stride, const void* k_pe
   a.loc = loc;
   a.n = n;
   a.thr = threshold;
-  a.kscale = ks;
+  a.kscale = lloyd_kscale(gain);
   a.codes = codes;
   a.params = params;
   a.k_pe = static_cast<const uint16_t*>(k_pe);
@@ -136,7 +139,66 @@ int rolaq_write_rows(const void* latent, int64_t latent_stride, const void* k_pe
   a.hp = static_cast<uint16_t*>(hp_c);
   a.row_of_slot = row_of_slot;
   a.owner_of_row = owner_of_row;
+  return a;
+}
+
+}  // namespace
+
+extern "C" {
+
+int rolaq_write_rows(const void* latent, int64_t latent_stride, const void* k_pe, int64_t pe_stride0,
+                     int64_t pe_stride1, const void* rotation_t, const int64_t* loc, const int64_t* seq_lens,
+                     const int64_t* positions, const int64_t* req_idx, int64_t n, int D, int R, int P, int W,
+                     int max_reqs, float threshold, double gain, uint8_t* codes, float* params, void* rope_buf,
+                     void* hp_c, int32_t* row_of_slot, int32_t* owner_of_row, void* stream) {
+  if (n < 0) return fail(ROLAQ_ERR_INVALID, "write_rows: n < 0");
+  if (n == 0) { g_err[0] = '\0'; return ROLAQ_OK; }
+  const int rc = check_writer("write_rows", latent, latent_stride, k_pe, rotation_t, loc, seq_lens, req_idx, D, R, P,
+                              W, max_reqs, threshold, gain, codes, params, rope_buf, hp_c, row_of_slot, owner_of_row);
+  if (rc != ROLAQ_OK) return rc;
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (!rotation_t) {
+    rolaq::AuxArgs aux{static_cast<const uint16_t*>(k_pe), pe_stride0, pe_stride1, seq_lens, positions, req_idx,
+                       R, P, W, max_reqs, static_cast<uint16_t*>(rope_buf), static_cast<uint16_t*>(hp_c),
+                       row_of_slot, owner_of_row};
+    return hip_status(rolaq_launch_pack_bf16_aux(static_cast<const uint16_t*>(latent), latent_stride, loc, n, D,
+                                                 threshold, lloyd_kscale(gain), codes, params, aux, s),
+                      "write_rows (un-rotated) launch");
+  }
+  const rolaq::WriterArgs a = writer_args(latent, latent_stride, k_pe, pe_stride0, pe_stride1, rotation_t, loc,
+                                          seq_lens, positions, req_idx, n, R, P, W, max_reqs, threshold, gain, codes,
+                                          params, rope_buf, hp_c, row_of_slot, owner_of_row);
   return hip_status(rolaq_launch_writer(a, D, cu_count(), s), "write_rows launch");
+}
+
+int rolaq_norm_write_rows(const void* kv_a, int64_t kv_a_stride, const void* norm_weight, float eps,
+                          void* latent_out, int64_t latent_out_stride, const void* k_pe, int64_t pe_stride0,
+                          int64_t pe_stride1, const void* rotation_t, const int64_t* loc, const int64_t* seq_lens,
+                          const int64_t* positions, const int64_t* req_idx, int64_t n, int D, int R, int P, int W,
+                          int max_reqs, float threshold, double gain, uint8_t* codes, float* params,
+                          void* rope_buf, void* hp_c, int32_t* row_of_slot, int32_t* owner_of_row, void* stream) {
+  if (n < 0) return fail(ROLAQ_ERR_INVALID, "norm_write_rows: n < 0");
+  if (n == 0) { g_err[0] = '\0'; return ROLAQ_OK; }
+  const int rc = check_writer("norm_write_rows", kv_a, kv_a_stride, k_pe, rotation_t, loc, seq_lens, req_idx, D, R,
+                              P, W, max_reqs, threshold, gain, codes, params, rope_buf, hp_c, row_of_slot,
+                              owner_of_row);
+  if (rc != ROLAQ_OK) return rc;
+  if (!rotation_t)
+    return fail(ROLAQ_ERR_INVALID, "norm_write_rows: rotation_t is required (the identity for an un-rotated layer)");
+  if (!norm_weight || !aligned(norm_weight, 16)) return fail(ROLAQ_ERR_INVALID, "norm_write_rows: norm_weight must be a 16-byte aligned pointer");
+  if (!(eps >= 0.0f) || !std::isfinite(eps)) return fail(ROLAQ_ERR_INVALID, "norm_write_rows: eps must be finite and >= 0");
+  if (latent_out &&
+      (latent_out_stride < D || latent_out_stride % 8 || latent_out_stride >= (1 << 24) || !aligned(latent_out, 16)))
+    return fail(ROLAQ_ERR_INVALID,
+                "norm_write_rows: latent_out must be 16-byte aligned with a row stride >= D, multiple of 8, below 2^24");
+  rolaq::WriterArgs a = writer_args(kv_a, kv_a_stride, k_pe, pe_stride0, pe_stride1, rotation_t, loc, seq_lens,
+                                    positions, req_idx, n, R, P, W, max_reqs, threshold, gain, codes, params,
+                                    rope_buf, hp_c, row_of_slot, owner_of_row);
+  a.gamma = static_cast<const uint16_t*>(norm_weight);
+  a.eps = eps;
+  a.y = static_cast<uint16_t*>(latent_out);
+  a.ys = latent_out_stride;
+  return hip_status(rolaq_launch_writer(a, D, cu_count(), static_cast<hipStream_t>(stream)), "norm_write_rows launch");
 }
 
 int rolaq_prepare_gf_splits(const int32_t* splits, int32_t* quant, int32_t* merge, int64_t n, void* stream) {

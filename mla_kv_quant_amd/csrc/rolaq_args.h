@@ -59,6 +59,13 @@ struct WriterArgs {
   int32_t* owner_of_row;
   int nstripes;
   int pe_vec;  // k_pe rows copied as dword pairs (set by the launcher)
+  // kv_a_layernorm fused in front of the rotation: x is the pre-norm kv_a
+  // row, gamma the norm weight [D] (bf16), or null for no norm; y [n, ys]
+  // receives the normalized rows (bf16), or null
+  const uint16_t* gamma;
+  float eps;
+  uint16_t* y;
+  int64_t ys;
 };
 
 struct ExtendArgs {

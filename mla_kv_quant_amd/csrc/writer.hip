@@ -44,6 +44,40 @@ __device__ __forceinline__ float sum_over_rows(float v) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// Sum over the four lanes 4r..4r+3 (DPP quad permutes); every lane of the
+// quad gets the same bits, (v0 + v1) + (v2 + v3) up to commutation.
+__device__ __forceinline__ float sum_over_quad(float v) {
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0xB1, 0xF, 0xF, true));  // [1,0,3,2]
+  v += __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x4E, 0xF, 0xF, true));  // [2,3,0,1]
+  return v;
+}
+
+// Sum of squares of eight bf16 values, FP32.
+__device__ __forceinline__ float sumsq8(u32x4 v) {
+  float s = 0.f;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    s = fmaf(bf16_lo(v[i]), bf16_lo(v[i]), s);
+    s = fmaf(bf16_hi(v[i]), bf16_hi(v[i]), s);
+  }
+  return s;
+}
+
+// kv_a_layernorm of eight bf16 values with the row's inverse RMS r and the
+// weights gm: bf16(gamma * bf16(x * r)), each rounding to nearest even -- the
+// cast order of DeepseekV2RMSNorm.forward (transformers
+// models/deepseek_v2/modeling_deepseek_v2.py:166-171). The product of two
+// bf16 values is exact in FP32, so the last step rounds once.
+__device__ __forceinline__ u32x4 rms_apply8(u32x4 v, float r, u32x4 gm) {
+  u32x4 o;
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint32_t h = pack_bf16(bf16_lo(v[i]) * r, bf16_hi(v[i]) * r);
+    o[i] = pack_bf16(bf16_lo(h) * bf16_lo(gm[i]), bf16_hi(h) * bf16_hi(gm[i]));
+  }
+  return o;
+}
+
 // floor(x) as int32 in one instruction (v_cvt_flr_i32_f32; saturates, which
 // the caller's clamp to 0..3 absorbs).
 __device__ __forceinline__ int floor_to_int(float x) {
@@ -58,6 +92,7 @@ struct WriterGeo {
   static constexpr int KS = D / 32;            // MFMA K-steps
   static constexpr int STRIDE = 2 * D + 16;    // bytes per LDS row (padded)
   static constexpr int LDS_BYTES = 128 * STRIDE;
+  static constexpr int LDS_NORM_BYTES = LDS_BYTES + 2 * D;  // + the norm weight
 };
 
 // Block = one quantization group g x a stripe of 64-row tiles. The block's
@@ -65,7 +100,13 @@ struct WriterGeo {
 // synchronise after staging. Blocks of the NG groups of one stripe get the same
 // blockIdx % 8, i.e. the same XCD, so each latent row is fetched from HBM once
 // and served to the other groups from that XCD's L2.
-template <int D>
+//
+// NORM: the rows are kv_a_layernorm inputs. Before a tile's K loop the wave
+// reads the tile's rows once more for their sums of squares (the four lanes
+// of a row each sum 8 columns per K-step, then a quad sum), and every K-step
+// chunk is normalized in registers before it becomes an MFMA operand; each
+// group's block also stores a quarter (1/NG) of the normalized rows' columns to y.
+template <int D, bool NORM>
 __global__ __launch_bounds__(64 * kWriterWaves, 1) void writer_kernel(WriterArgs a) {
   using G = WriterGeo<D>;
   constexpr int NG = G::NG, KS = G::KS, STR = G::STRIDE;
@@ -95,6 +136,11 @@ __global__ __launch_bounds__(64 * kWriterWaves, 1) void writer_kernel(WriterArgs
       *reinterpret_cast<u32x4*>(s_rt + m * STR + off) =
           *reinterpret_cast<const u32x4*>(src + col * (2 * D) + off);
     }
+  }
+  uint8_t* s_gamma = s_rt + G::LDS_BYTES;
+  if constexpr (NORM) {
+    for (int c = tid; c < D / 8; c += 64 * kWriterWaves)
+      *reinterpret_cast<u32x4*>(s_gamma + 16 * c) = *reinterpret_cast<const u32x4*>(a.gamma + 8 * c);
   }
   __syncthreads();
 
@@ -130,6 +176,13 @@ __global__ __launch_bounds__(64 * kWriterWaves, 1) void writer_kernel(WriterArgs
                  (uint32_t)__builtin_amdgcn_ds_bpermute(perm, (int)v.z),
                  (uint32_t)__builtin_amdgcn_ds_bpermute(perm, (int)v.w)};
   };
+  // normalized rows go out in the K-steps ks with ks % NG == g of each group's
+  // block (the stores shared out, so no block's loads wait behind all of
+  // them), lanes 4r..4r+3 storing the 64 contiguous bytes of row r of one
+  // K-step (the load pattern)
+  const bool ystore = NORM && a.y != nullptr;
+  const int yrow = (int)a.ys * 2;
+  const int yoff = (lane >> 2) * yrow + 16 * (lane & 3);
   u32x4 xb[kWriterDepth][4];
   int64_t t = (int64_t)stripe * kWriterWaves + wave;
   {
@@ -151,6 +204,34 @@ __global__ __launch_bounds__(64 * kWriterWaves, 1) void writer_kernel(WriterArgs
     const int64_t row0 = t * kWriterRows;
     const __amdgpu_buffer_rsrc_t rs = tile_rsrc(t), rn = tile_rsrc(t + tstep);
 
+    // ---- NORM: inverse RMS of rows 16 nb + lane / 4 (rows past n read as 0) -----
+    float rinv[4];
+    __amdgpu_buffer_rsrc_t ys_rsrc;
+    if constexpr (NORM) {
+      if (ystore) {
+        const int64_t rows = min((int64_t)kWriterRows, a.n - row0);
+        ys_rsrc = __builtin_amdgcn_make_buffer_rsrc(a.y + row0 * a.ys, (short)0, (int)(rows * yrow), kBufferFlags);
+      }
+    }
+    if constexpr (NORM) {
+      float ss[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int k0 = 0; k0 < KS; k0 += 2) {
+        u32x4 v[2][4];
+#pragma unroll
+        for (int k = 0; k < 2; ++k)
+#pragma unroll
+          for (int nb = 0; nb < 4; ++nb) v[k][nb] = xload(rs, nb, k0 + k);
+#pragma unroll
+        for (int k = 0; k < 2; ++k)
+#pragma unroll
+          for (int nb = 0; nb < 4; ++nb) ss[nb] += sumsq8(v[k][nb]);
+      }
+#pragma unroll
+      for (int nb = 0; nb < 4; ++nb)
+        rinv[nb] = 1.0f / sqrtf(sum_over_quad(ss[nb]) * (1.0f / D) + a.eps);
+    }
+
     // ---- C^T tile: 128 columns x 64 rows on MFMA 16x16x32 ----------------------
     f32x4 acc[8][4];
 #pragma unroll
@@ -163,6 +244,17 @@ __global__ __launch_bounds__(64 * kWriterWaves, 1) void writer_kernel(WriterArgs
       u32x4 av[8], xv[4];
 #pragma unroll
       for (int mb = 0; mb < 8; ++mb) av[mb] = *reinterpret_cast<const u32x4*>(lds_a + 16 * mb * STR + 64 * ks);
+      if constexpr (NORM) {
+        const u32x4 gm = *reinterpret_cast<const u32x4*>(s_gamma + 64 * ks + 16 * (lane & 3));
+#pragma unroll
+        for (int nb = 0; nb < 4; ++nb) {
+          xb[cur][nb] = rms_apply8(xb[cur][nb], rinv[nb], gm);
+          if (ystore && ks % NG == g)  // rows at or past n fall outside the buffer and are dropped
+            __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(__attribute__((ext_vector_type(4))) uint32_t,
+                                                                      xb[cur][nb]),
+                                                   ys_rsrc, yoff + 64 * ks, nb * 16 * yrow, 0);
+        }
+      }
 #pragma unroll
       for (int nb = 0; nb < 4; ++nb) xv[nb] = relayout(xb[cur][nb]);
       const int kk = ks + kWriterDepth;
@@ -282,17 +374,19 @@ hipError_t rolaq_launch_writer(const rolaq::WriterArgs& args_in, int D, int num_
   a.pe_vec = a.pe_s1 == 1 && a.R == 16 * NG && (a.pe_s0 % 4) == 0 &&
              (reinterpret_cast<uintptr_t>(a.k_pe) % 8) == 0 && (reinterpret_cast<uintptr_t>(a.rope) % 8) == 0;
   const dim3 grid((unsigned)(stripes * NG)), block(64 * kWriterWaves);
-#define ROLAQ_WRITER(DD)                                                                               \
-  if (D == DD) {                                                                                      \
-    const int lds = WriterGeo<DD>::LDS_BYTES;                                                         \
-    const hipError_t e =                                                                              \
-        hipFuncSetAttribute((const void*)writer_kernel<DD>, hipFuncAttributeMaxDynamicSharedMemorySize, lds); \
-    if (e != hipSuccess) return e;                                                                    \
-    hipLaunchKernelGGL((writer_kernel<DD>), grid, block, lds, stream, a);                             \
-    return hipGetLastError();                                                                         \
+#define ROLAQ_WRITER(DD, NORM, LDS)                                                                         \
+  if (D == DD && (a.gamma != nullptr) == NORM) {                                                           \
+    const int lds = WriterGeo<DD>::LDS;                                                                    \
+    const hipError_t e = hipFuncSetAttribute((const void*)writer_kernel<DD, NORM>,                         \
+                                             hipFuncAttributeMaxDynamicSharedMemorySize, lds);             \
+    if (e != hipSuccess) return e;                                                                         \
+    hipLaunchKernelGGL((writer_kernel<DD, NORM>), grid, block, lds, stream, a);                            \
+    return hipGetLastError();                                                                              \
   }
-  ROLAQ_WRITER(512)
-  ROLAQ_WRITER(256)
+  ROLAQ_WRITER(512, false, LDS_BYTES)
+  ROLAQ_WRITER(256, false, LDS_BYTES)
+  ROLAQ_WRITER(512, true, LDS_NORM_BYTES)
+  ROLAQ_WRITER(256, true, LDS_NORM_BYTES)
 #undef ROLAQ_WRITER
   return hipErrorInvalidValue;
 }

@@ -8,6 +8,7 @@ no synchronisation, no host branch on device data.
 from __future__ import annotations
 
 import ctypes
+import math
 
 import torch
 
@@ -59,13 +60,9 @@ def scatter_pack_rows(x: torch.Tensor, slots: torch.Tensor, codes: torch.Tensor,
         _p(codes), _p(params), _stream(x)))
 
 
-def write_rows(latent: torch.Tensor, k_pe: torch.Tensor, rotation_t: torch.Tensor | None,
-               loc: torch.Tensor, seq_lens: torch.Tensor, positions: torch.Tensor | None,
-               req_idx: torch.Tensor, codes: torch.Tensor, params: torch.Tensor,
-               rope_buf: torch.Tensor, hp_c: torch.Tensor, row_of_slot: torch.Tensor,
-               owner_of_row: torch.Tensor, P: int, W: int, max_reqs: int,
-               threshold: float, gain: float) -> None:
-    """Fused rotate + quantize + pack + rope/window stores for ``n`` rows."""
+def _check_writer(latent, k_pe, rotation_t, loc, seq_lens, positions, req_idx, codes, params, rope_buf, hp_c,
+                  row_of_slot, owner_of_row, P, W, max_reqs) -> None:
+    """Shape, dtype and device checks shared by the writer entry points."""
     dev = latent.device
     _need(latent, "latent", torch.bfloat16, dev, 2)
     n, D = latent.shape
@@ -104,11 +101,61 @@ def write_rows(latent: torch.Tensor, k_pe: torch.Tensor, rotation_t: torch.Tenso
         raise ValueError("hp_c / owner_of_row are smaller than 1 + max_reqs * (P + W)")
     if latent.stride(1) != 1:
         raise ValueError("latent rows must be contiguous")
+
+
+def write_rows(latent: torch.Tensor, k_pe: torch.Tensor, rotation_t: torch.Tensor | None,
+               loc: torch.Tensor, seq_lens: torch.Tensor, positions: torch.Tensor | None,
+               req_idx: torch.Tensor, codes: torch.Tensor, params: torch.Tensor,
+               rope_buf: torch.Tensor, hp_c: torch.Tensor, row_of_slot: torch.Tensor,
+               owner_of_row: torch.Tensor, P: int, W: int, max_reqs: int,
+               threshold: float, gain: float) -> None:
+    """Fused rotate + quantize + pack + rope/window stores for ``n`` rows."""
+    _check_writer(latent, k_pe, rotation_t, loc, seq_lens, positions, req_idx, codes, params, rope_buf, hp_c,
+                  row_of_slot, owner_of_row, P, W, max_reqs)
+    n, D = latent.shape
+    R = k_pe.shape[1]
     _lib.check(_lib.load().rolaq_write_rows(
         _p(latent), latent.stride(0), _p(k_pe), k_pe.stride(0), k_pe.stride(1), _p(rotation_t),
         _p(loc), _p(seq_lens), _p(positions), _p(req_idx), n, D, R, int(P), int(W), int(max_reqs),
         float(threshold), float(gain), _p(codes), _p(params), _p(rope_buf), _p(hp_c),
         _p(row_of_slot), _p(owner_of_row), _stream(latent)))
+
+
+def norm_write_rows(kv_a: torch.Tensor, norm_weight: torch.Tensor, eps: float, latent_out: torch.Tensor | None,
+                    k_pe: torch.Tensor, rotation_t: torch.Tensor, loc: torch.Tensor, seq_lens: torch.Tensor,
+                    positions: torch.Tensor | None, req_idx: torch.Tensor, codes: torch.Tensor, params: torch.Tensor,
+                    rope_buf: torch.Tensor, hp_c: torch.Tensor, row_of_slot: torch.Tensor,
+                    owner_of_row: torch.Tensor, P: int, W: int, max_reqs: int,
+                    threshold: float, gain: float) -> None:
+    """kv_a_layernorm + rotate + quantize + pack + rope/window stores for ``n`` rows.
+
+    ``kv_a`` holds the pre-norm rows; ``latent_out`` (or None) receives the
+    normalized bf16 rows. The cache arguments are those of :func:`write_rows`.
+    """
+    dev = kv_a.device
+    _need(kv_a, "kv_a", torch.bfloat16, dev, 2)
+    n, D = kv_a.shape
+    _need(norm_weight, "norm_weight", torch.bfloat16, dev, 1)
+    _contig(norm_weight, "norm_weight")
+    if norm_weight.numel() != D:
+        raise ValueError("norm_weight must have D entries")
+    if rotation_t is None:
+        raise ValueError("rotation_t is required (the identity for an un-rotated layer)")
+    if latent_out is not None:
+        _need(latent_out, "latent_out", torch.bfloat16, dev, 2)
+        if tuple(latent_out.shape) != (n, D) or latent_out.stride(1) != 1:
+            raise ValueError("latent_out must be [n, D] with contiguous rows")
+    if not math.isfinite(eps) or eps < 0:
+        raise ValueError("eps must be finite and >= 0")
+    # the shared checks of write_rows, then the fused launch
+    _check_writer(kv_a, k_pe, rotation_t, loc, seq_lens, positions, req_idx, codes, params, rope_buf, hp_c,
+                  row_of_slot, owner_of_row, P, W, max_reqs)
+    _lib.check(_lib.load().rolaq_norm_write_rows(
+        _p(kv_a), kv_a.stride(0), _p(norm_weight), float(eps), _p(latent_out),
+        latent_out.stride(0) if latent_out is not None else 0, _p(k_pe), k_pe.stride(0), k_pe.stride(1),
+        _p(rotation_t), _p(loc), _p(seq_lens), _p(positions), _p(req_idx), n, D, k_pe.shape[1], int(P), int(W),
+        int(max_reqs), float(threshold), float(gain), _p(codes), _p(params), _p(rope_buf), _p(hp_c),
+        _p(row_of_slot), _p(owner_of_row), _stream(kv_a)))
 
 
 def prepare_gf_splits(splits: torch.Tensor, quant: torch.Tensor, merge: torch.Tensor) -> None:

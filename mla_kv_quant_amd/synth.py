@@ -48,6 +48,26 @@ def make_latent(n: int, width: int, outliers: int, seed: int, factor: float = 20
     return x.to(torch.bfloat16)
 
 
+def make_kv_a(n: int, width: int, seed: int, device="cpu") -> torch.Tensor:
+    """bf16 pre-norm compressed latents ``kv_a``: N(0, 0.05^2) rows with a few
+    channels x20, and per-row magnitudes spread over two octaves."""
+    g = torch.Generator(device=device).manual_seed(seed)
+    x = torch.randn(n, width, generator=g, device=device, dtype=torch.float32) * 0.05
+    ch = outlier_channels(width, max(1, width // 100), seed + 7).to(device)
+    x[:, ch] *= 20.0
+    x *= torch.exp2(torch.rand(n, 1, generator=g, device=device) * 2.0 - 1.0)
+    return x.to(torch.bfloat16)
+
+
+def make_norm_weight(width: int, seed: int, device="cpu") -> torch.Tensor:
+    """bf16 ``kv_a_layernorm`` weight: |N(1, 0.3^2)| with a few channels x8
+    (the post-norm latent's outlier channels come from the weight)."""
+    g = torch.Generator().manual_seed(seed)
+    w = (torch.randn(width, generator=g) * 0.3 + 1.0).abs()
+    w[outlier_channels(width, max(1, width // 100), seed + 3)] *= 8.0
+    return w.to(torch.bfloat16).to(device)
+
+
 def make_normal(shape, seed: int, std: float = 1.0, device="cpu",
                 dtype=torch.bfloat16) -> torch.Tensor:
     g = torch.Generator(device=device).manual_seed(seed)

@@ -37,14 +37,17 @@ def _write_rotation(pool, layer_id: int, r: torch.Tensor | None):
     return cached[layer_id][1]
 
 
-def try_fast_decode_store(pool, layer_id, loc, c_kv, k_pe) -> bool:
-    """Return whether the decode write was handled; the caller falls back otherwise.
+def _identity_rotation(pool, device) -> torch.Tensor:
+    """bf16 identity for un-rotated layers on the fused-norm path (x * I is exact)."""
+    eye = getattr(pool, "_fast_write_identity", None)
+    if eye is None:
+        eye = pool._fast_write_identity = torch.eye(pool.kv_lora_rank, dtype=torch.bfloat16, device=device)
+    return eye
 
-    One launch rotates (bf16 MFMA), quantizes, packs and stores rope, window row
-    and ring ownership for every row of this decode step.
-    """
+
+def _decode_handled(pool, n: int) -> bool:
+    """The gatekeeping of mla_fused_writer.py:117-134 for a decode step of ``n`` rows."""
     meta = pool._fb_window_meta
-    n = c_kv.numel() // pool.kv_lora_rank
     if (
         n <= 0
         or (pool.kv_lora_rank, pool.qk_rope_head_dim) not in SUPPORTED_DIMS
@@ -60,7 +63,17 @@ def try_fast_decode_store(pool, layer_id, loc, c_kv, k_pe) -> bool:
         or pool._audit_budget > 0
     ):
         return False
-    if not (pool._lloyd_max and pool._bits == 2):
+    return bool(pool._lloyd_max and pool._bits == 2)
+
+
+def try_fast_decode_store(pool, layer_id, loc, c_kv, k_pe) -> bool:
+    """Return whether the decode write was handled; the caller falls back otherwise.
+
+    One launch rotates (bf16 MFMA), quantizes, packs and stores rope, window row
+    and ring ownership for every row of this decode step.
+    """
+    meta = pool._fb_window_meta
+    if not _decode_handled(pool, c_kv.numel() // pool.kv_lora_rank):
         return False
     li = layer_id - pool.start_layer
     r = pool.latent_rotation(layer_id, local=True)
@@ -106,6 +119,61 @@ def write_prefill(pool, layer_id, loc, c_kv, k_pe, positions, seq_lens, req_pool
         x, pe, rt, _as_int64(loc), _as_int64(seq_lens), _as_int64(positions), _as_int64(req_pool_indices),
         pool.c_codes[li], pool.c_params[li], pool.rope_buf[li], pool.hp_c[li], pool.hp_row_of_slot,
         pool.hp_owner_of_row, pool._win_p, pool._win_r, pool._max_reqs, t, g)
+
+
+def _quantizer(pool, li: int):
+    params = pool._rolaq_quantizers[li]
+    return (params[0], params[1]) if params is not None else (LM_THRESHOLD, LM_GAIN)
+
+
+def try_fast_norm_decode_store(pool, layer_id, loc, kv_a, k_pe, norm_weight, eps, latent_out=None) -> bool:
+    """``try_fast_decode_store(pool, layer_id, loc, kv_a_layernorm(kv_a), k_pe)`` in one launch.
+
+    ``kv_a`` is the pre-norm compressed latent; ``norm_weight``/``eps`` are the
+    layer's ``kv_a_layernorm`` (DeepseekV2RMSNorm) weight (bf16 [D]) and
+    epsilon. ``latent_out`` ([n, D] bf16, or None) receives the normalized rows.
+    Same gatekeeping as :func:`try_fast_decode_store`; ``False`` = not handled.
+    """
+    meta = pool._fb_window_meta
+    if not _decode_handled(pool, kv_a.numel() // pool.kv_lora_rank):
+        return False
+    li = layer_id - pool.start_layer
+    r = pool.latent_rotation(layer_id, local=True)
+    rt = _write_rotation(pool, layer_id, r)
+    if rt is None:
+        rt = _identity_rotation(pool, kv_a.device)
+    loc64 = _as_int64(loc)
+    pool._write_loc = loc64
+    x = kv_a.reshape(-1, pool.kv_lora_rank)
+    if x.dtype != torch.bfloat16:
+        x = x.to(torch.bfloat16)
+    t, g = _quantizer(pool, li)
+    kernels.norm_write_rows(
+        x, norm_weight, float(eps), latent_out, k_pe.reshape(-1, pool.qk_rope_head_dim), rt, loc64,
+        _as_int64(meta["seq_lens"]), None, _as_int64(meta["req_pool_indices"]), pool.c_codes[li],
+        pool.c_params[li], pool.rope_buf[li], pool.hp_c[li], pool.hp_row_of_slot, pool.hp_owner_of_row,
+        pool._win_p, pool._win_r, pool._max_reqs, t, g)
+    return True
+
+
+def norm_write_prefill(pool, layer_id, loc, kv_a, k_pe, positions, seq_lens, req_pool_indices, norm_weight, eps,
+                       latent_out=None) -> None:
+    """:func:`write_prefill` of ``kv_a_layernorm(kv_a)`` in one launch (see
+    :func:`try_fast_norm_decode_store` for the norm arguments)."""
+    li = layer_id - pool.start_layer
+    r = pool.latent_rotation(layer_id, local=True)
+    rt = _write_rotation(pool, layer_id, r)
+    if rt is None:
+        rt = _identity_rotation(pool, kv_a.device)
+    x = kv_a.reshape(-1, pool.kv_lora_rank)
+    if x.dtype != torch.bfloat16:
+        x = x.to(torch.bfloat16)
+    t, g = _quantizer(pool, li)
+    kernels.norm_write_rows(
+        x, norm_weight, float(eps), latent_out, k_pe.reshape(-1, pool.qk_rope_head_dim), rt, _as_int64(loc),
+        _as_int64(seq_lens), _as_int64(positions), _as_int64(req_pool_indices), pool.c_codes[li],
+        pool.c_params[li], pool.rope_buf[li], pool.hp_c[li], pool.hp_row_of_slot, pool.hp_owner_of_row,
+        pool._win_p, pool._win_r, pool._max_reqs, t, g)
 
 
 def scatter_pack_rows(x, slots, codes_buf, params_buf, group_size, lloyd_max, bits=2, quantizer_params=None):

@@ -5,7 +5,10 @@ TEST INFRASTRUCTURE ONLY (see ``oracle/__init__.py``).
 Restates ``mla_quant/oscar.py:104-144`` (constants and the QDQ codec),
 ``mla_quant/quantizer.py:31-35`` (gain snapping), ``:102-124`` (cast order of
 ``rotate_quantize``), ``:145-152`` (rotation validation) and
-``mla_quant/train.py:21-29`` (``signal_gain``).
+``mla_quant/train.py:21-29`` (``signal_gain``), and ``kv_a_layernorm``: the
+third-party ``DeepseekV2RMSNorm.forward`` (transformers 5.15.0,
+``models/deepseek_v2/modeling_deepseek_v2.py:166-171``) whose output the
+reference quantizes (``mla_quant/objectives.py:25-29``, ``calibrate.py:40``).
 """
 
 from __future__ import annotations
@@ -126,6 +129,20 @@ def rotate_quantize(latent: torch.Tensor, rotation: torch.Tensor,
     if high_precision_mask is None:
         return restored
     return torch.where(mask.unsqueeze(-1), latent, restored)
+
+
+def kv_a_layernorm(x: torch.Tensor, weight: torch.Tensor, eps: float = 1e-6) -> torch.Tensor:
+    """RMS norm with the cast order of DeepseekV2RMSNorm.forward (transformers
+    5.15.0, models/deepseek_v2/modeling_deepseek_v2.py:166-171).
+
+    Statistics in FP32 (``mean(x^2)`` over the last dim, ``rsqrt(var + eps)``),
+    the normalized row rounded to the input dtype, then multiplied by the
+    weight in the weight's dtype: ``bf16(w * bf16(x * r))`` for bf16 inputs.
+    CPU torch ops (``rsqrt`` on CPU is ``1 / sqrt`` in FP32).
+    """
+    h = x.to(torch.float32)
+    r = torch.rsqrt(h.pow(2).mean(-1, keepdim=True) + eps)
+    return weight * (h * r).to(x.dtype)
 
 
 def signal_gain(threshold) -> float:

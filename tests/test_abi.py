@@ -19,7 +19,7 @@ def declared_symbols():
 def test_header_declares_the_entry_points():
     syms = declared_symbols()
     for name in ("rolaq_last_error", "rolaq_abi_version", "rolaq_scatter_pack_rows", "rolaq_write_rows",
-                 "rolaq_prepare_gf_splits", "rolaq_decode_fwd", "rolaq_decode_partials", "rolaq_decode_merge", "rolaq_extend_fwd",
+                 "rolaq_norm_write_rows", "rolaq_prepare_gf_splits", "rolaq_decode_fwd", "rolaq_decode_partials", "rolaq_decode_merge", "rolaq_extend_fwd",
                  "rolaq_assemble_rows"):
         assert name in syms
 
@@ -66,6 +66,25 @@ def test_invalid_arguments_are_rejected_before_any_launch():
     assert lib.rolaq_decode_merge(p, p, p, 8, 4, 16, 384, p, 8192, 512, None) == _lib.ROLAQ_ERR_INVALID
     assert lib.rolaq_decode_merge(None, p, p, 8, 4, 16, 512, p, 8192, 512, None) == _lib.ROLAQ_ERR_INVALID
     assert lib.rolaq_decode_merge(None, None, None, 8, 0, 16, 512, None, 0, 0, None) == _lib.ROLAQ_OK
+    # fused norm writer: rotation and norm weight are required, eps must be finite
+    wargs = [p, 512, p, 1e-6, None, 0, p, 64, 1, p, p, p, None, p, 8, 512, 64, 4, 16, 8, 0.98, 1.16, p, p, p, p,
+             p, p, None]
+    assert lib.rolaq_norm_write_rows(*(wargs[:14] + [0] + wargs[15:])) == _lib.ROLAQ_OK  # n == 0
+    bad = list(wargs)
+    bad[9] = None
+    assert lib.rolaq_norm_write_rows(*bad) == _lib.ROLAQ_ERR_INVALID and b"rotation_t" in lib.rolaq_last_error()
+    bad = list(wargs)
+    bad[2] = None
+    assert lib.rolaq_norm_write_rows(*bad) == _lib.ROLAQ_ERR_INVALID and b"norm_weight" in lib.rolaq_last_error()
+    bad = list(wargs)
+    bad[3] = float("inf")
+    assert lib.rolaq_norm_write_rows(*bad) == _lib.ROLAQ_ERR_INVALID and b"eps" in lib.rolaq_last_error()
+    bad = list(wargs)
+    bad[4], bad[5] = p, 100
+    assert lib.rolaq_norm_write_rows(*bad) == _lib.ROLAQ_ERR_INVALID and b"latent_out" in lib.rolaq_last_error()
+    bad = list(wargs)
+    bad[15] = 384
+    assert lib.rolaq_norm_write_rows(*bad) == _lib.ROLAQ_ERR_INVALID and b"(D, R)" in lib.rolaq_last_error()
     # extend: shape and pointer checks, empty batch is a no-op
     eargs = [p, 40 * 288, 288, p, 288, p, p, p, 16, p, p, p, p, p, p, 4, 40, 256, 32, 4, 16, 2048, 0.1, p,
              40 * 256, 256, None]
