@@ -466,12 +466,26 @@ def writer_result(args, dev: str) -> dict:
         "hbm_frac": round(wach / HBM_PEAK_GBS, 4),
         "mfma_frac": round(wb.flops_per_layer() / (wus * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
     }
+    # dequantize-rows of the cache just written (MHA prefill over a quantized
+    # prefix): every cfg1 row of one layer, rotated frame and rotated back
+    from mla_kv_quant_amd import kernels
+
+    d0 = wb.layers_data[0]
+    r_eff = d0["rt"].t().contiguous()
+    rows = torch.empty(wb.n, wb.D + wb.R, dtype=torch.bfloat16, device=dev)
+    for key, rot in (("assemble_us", None), ("assemble_unrotate_us", r_eff)):
+        ams = time_loop(lambda: kernels.assemble_rows(wb.loc, d0["codes"], d0["params"], d0["rope"], d0["hp"],
+                                                      d0["row"], d0["owner"], rot, rows),
+                        max(5, args.steps), args.warmup)
+        res[key] = round(ams * 1000.0, 3)
+    del rows
     for key, rows_out in (("norm_fused_us_per_layer", False), ("norm_fused_rows_out_us_per_layer", True)):
         nms = time_loop(lambda: wb.norm_step(rows_out), max(3, args.steps // 2), args.warmup)
         res[key] = round(nms * 1000.0 / args.layers, 3)
     print(f"[bench] writer: {wus:.2f} us/layer, {res['mtokens_per_s']} Mtok/s; with kv_a_layernorm fused: "
           f"{res['norm_fused_us_per_layer']} us/layer, and the normalized rows stored: "
-          f"{res['norm_fused_rows_out_us_per_layer']} us/layer", file=sys.stderr, flush=True)
+          f"{res['norm_fused_rows_out_us_per_layer']} us/layer; dequantize rows {res['assemble_us']} us, rotated "
+          f"back {res['assemble_unrotate_us']} us", file=sys.stderr, flush=True)
     del wb
     torch.cuda.empty_cache()
     return res

@@ -26,6 +26,47 @@ from .writer import LM_GAIN, LM_THRESHOLD, SUPPORTED_DIMS
 
 GROUP_SIZE = 128
 
+# Read-only helper tensors per (device, D), grown to the largest row count
+# seen: the slot ids 1..n, seq_len 1, request 0, zero rope keys and an empty
+# window. The writer writes row_of_slot[slot] = -1 for these rows (no window:
+# P = W = 0), the value it already holds, so sharing them across calls and
+# streams is safe.
+_HELPERS: dict = {}
+
+
+# bf16 R_eff and its transpose on the device, per rotation tensor (held, so
+# its id stays unique) and its version counter (an in-place update re-derives).
+_ROTATIONS: dict = {}
+
+
+def _rotation_operands(rotation: torch.Tensor, dev: torch.device):
+    key = (id(rotation), rotation._version, str(dev))
+    hit = _ROTATIONS.get(key)
+    if hit is None:
+        r_eff = rotation.to(device=dev, dtype=torch.bfloat16).contiguous()
+        if len(_ROTATIONS) >= 16:
+            _ROTATIONS.pop(next(iter(_ROTATIONS)))
+        hit = _ROTATIONS[key] = (rotation, r_eff, r_eff.t().contiguous())
+    return hit[1], hit[2]
+
+
+def _helpers(dev: torch.device, n: int, D: int, R: int):
+    key = (str(dev), D)
+    h = _HELPERS.get(key)
+    if h is None or h["cap"] < n:
+        cap = max(n, 2 * h["cap"] if h else 0)
+        h = _HELPERS[key] = {
+            "cap": cap,
+            "slots": torch.arange(1, cap + 1, dtype=torch.int64, device=dev),
+            "ones": torch.ones(cap, dtype=torch.int64, device=dev),
+            "zeros": torch.zeros(cap, dtype=torch.int64, device=dev),
+            "pe": torch.zeros(cap, R, dtype=torch.bfloat16, device=dev),
+            "row": torch.full((cap + 1,), -1, dtype=torch.int32, device=dev),
+            "hp": torch.empty(1, D, dtype=torch.bfloat16, device=dev),
+            "owner": torch.zeros(1, dtype=torch.int32, device=dev),
+        }
+    return h
+
 
 def rotate_quantize(latent: torch.Tensor, rotation: torch.Tensor, threshold: float = LM_THRESHOLD,
                     gain: float = LM_GAIN, high_precision_mask: torch.Tensor | None = None,
@@ -55,21 +96,17 @@ def rotate_quantize(latent: torch.Tensor, rotation: torch.Tensor, threshold: flo
     n = x.shape[0]
     if n == 0:
         return latent.clone()
-    r_eff = rotation.to(device=dev, dtype=torch.bfloat16)
+    r_eff, r_eff_t = _rotation_operands(rotation, dev)
+    h = _helpers(dev, n, D, R)
+    slots = h["slots"][:n]
     # scratch cache: slots 1..n (slot 0 is the padding slot), no BF16 window
     codes = torch.empty(n + 1, D // 4, dtype=torch.uint8, device=dev)
     params = torch.empty(n + 1, D // GROUP_SIZE, 2, dtype=torch.float32, device=dev)
     rope = torch.empty(n + 1, R, dtype=torch.bfloat16, device=dev)
-    hp = torch.empty(1, D, dtype=torch.bfloat16, device=dev)
-    row = torch.full((n + 1,), -1, dtype=torch.int32, device=dev)
-    owner = torch.zeros(1, dtype=torch.int32, device=dev)
-    slots = torch.arange(1, n + 1, dtype=torch.int64, device=dev)
-    ones = torch.ones(n, dtype=torch.int64, device=dev)
-    kernels.write_rows(x, torch.zeros(n, R, dtype=torch.bfloat16, device=dev), r_eff.t().contiguous(), slots, ones,
-                       None, torch.zeros(n, dtype=torch.int64, device=dev), codes, params, rope, hp, row, owner,
-                       0, 0, 1, float(threshold), float(gain))
+    kernels.write_rows(x, h["pe"][:n], r_eff_t, slots, h["ones"][:n], None, h["zeros"][:n], codes,
+                       params, rope, h["hp"], h["row"][:n + 1], h["owner"], 0, 0, 1, float(threshold), float(gain))
     out = torch.empty(n, D + R, dtype=torch.bfloat16, device=dev)
-    kernels.assemble_rows(slots, codes, params, rope, hp, row, owner, r_eff.contiguous(), out)
+    kernels.assemble_rows(slots, codes, params, rope, h["hp"], h["row"][:n + 1], h["owner"], r_eff, out)
     restored = out[:, :D].reshape(latent.shape)
     if mask is None:
         return restored
