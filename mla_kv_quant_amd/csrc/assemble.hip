@@ -66,7 +66,8 @@ __global__ __launch_bounds__(256) void assemble_kernel(AssembleArgs a) {
 // output columns over all 128 rows -- MFMA 16x16x32 with R_eff rows as the A
 // operand, streamed from global memory (L2-resident, shared by all blocks) one
 // K-step ahead, and the LDS rows as the B operand. Per K-step and wave: D/128
-// R loads of 16 bytes per lane, 8 LDS reads, 8 D/128 MFMAs.
+// R loads of 16 bytes per lane (and 4 D/128 ds_bpermute), 8 LDS reads,
+// 8 D/128 MFMAs.
 // ---------------------------------------------------------------------------
 constexpr int kAsmRotRows = 128;
 constexpr int kAsmRotWaves = 8;
@@ -90,13 +91,23 @@ __global__ __launch_bounds__(64 * kAsmRotWaves, 1) void assemble_rot_kernel(Asse
   const int gq = lane >> 4, la = lane & 15;
   const int64_t row0 = (int64_t)blockIdx.x * kAsmRotRows;
 
-  // this wave's R_eff rows c0 + 16 mb + la; the first K-step's operands are in
-  // flight during the gather
+  // This wave's R_eff rows c0 + 16 mb + (0..15). They are loaded coalesced --
+  // lanes 4r..4r+3 read the 64 contiguous bytes of row r for one K-step, so a
+  // 16-lane pass touches 4 rows, not 16 -- and moved to the MFMA lane layout
+  // (lane la + 16 gq <- lane 4 la + gq) with ds_bpermute. The first K-step's
+  // loads are in flight during the gather.
   const int c0 = CW * wave;
-  const uint16_t* rbase = a.rot + (int64_t)(c0 + la) * D + 8 * gq;
-  u32x4 ra[2][MB];
+  const uint16_t* rbase = a.rot + (int64_t)(c0 + (lane >> 2)) * D + 8 * (lane & 3);
+  const int perm = 4 * (4 * la + gq);
+  auto relayout = [&](u32x4 v) {
+    return u32x4{(uint32_t)__builtin_amdgcn_ds_bpermute(perm, (int)v.x),
+                 (uint32_t)__builtin_amdgcn_ds_bpermute(perm, (int)v.y),
+                 (uint32_t)__builtin_amdgcn_ds_bpermute(perm, (int)v.z),
+                 (uint32_t)__builtin_amdgcn_ds_bpermute(perm, (int)v.w)};
+  };
+  u32x4 rr[2][MB];  // raw (load-layout) R chunks, one K-step ahead
 #pragma unroll
-  for (int mb = 0; mb < MB; ++mb) ra[0][mb] = gload<u32x4>(rbase + 16 * mb * D);
+  for (int mb = 0; mb < MB; ++mb) rr[0][mb] = gload<u32x4>(rbase + 16 * mb * D);
 
   // ---- per-row source: the window row while the slot owns it, else INT2 ---------
   if (tid < kAsmRotRows) {
@@ -182,9 +193,12 @@ __global__ __launch_bounds__(64 * kAsmRotWaves, 1) void assemble_rot_kernel(Asse
 #pragma unroll
   for (int ks = 0; ks < KS; ++ks) {
     const int cur = ks & 1;
+    u32x4 ra[MB];
+#pragma unroll
+    for (int mb = 0; mb < MB; ++mb) ra[mb] = relayout(rr[cur][mb]);
     if (ks + 1 < KS) {
 #pragma unroll
-      for (int mb = 0; mb < MB; ++mb) ra[cur ^ 1][mb] = gload<u32x4>(rbase + 16 * mb * D + 32 * (ks + 1));
+      for (int mb = 0; mb < MB; ++mb) rr[cur ^ 1][mb] = gload<u32x4>(rbase + 16 * mb * D + 32 * (ks + 1));
 #pragma unroll
       for (int nb = 0; nb < NB; ++nb)
         xv[cur ^ 1][nb] = *reinterpret_cast<const u32x4*>(xb + 16 * nb * STR + 64 * (ks + 1));
@@ -192,7 +206,7 @@ __global__ __launch_bounds__(64 * kAsmRotWaves, 1) void assemble_rot_kernel(Asse
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-      for (int mb = 0; mb < MB; ++mb) acc[mb][nb] = mfma16x16x32(ra[cur][mb], xv[cur][nb], acc[mb][nb]);
+      for (int mb = 0; mb < MB; ++mb) acc[mb][nb] = mfma16x16x32(ra[mb], xv[cur][nb], acc[mb][nb]);
     __builtin_amdgcn_sched_barrier(0);
   }
   // lane (la, gq) holds columns c0 + 16 mb + 4 gq + (0..3) of row 16 nb + la
