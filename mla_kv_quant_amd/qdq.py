@@ -15,6 +15,14 @@ kernels instead of torch CPU/GPU ops:
 
 Only the summation order differs from the reference, so codes agree except for
 rare +-1 flips at rounding boundaries (the writer's parity bar).
+
+``LearnedRotationQuantizer`` is the GPU counterpart of the reference's
+inference quantizer of the same name (mla_quant/quantizer.py:218-316): built
+from an artifact directory, ``quantize_layer(tensor, layer_idx, "nope")`` is
+what the HF fake-quantized cache calls for every appended latent row
+(``FakeQuantizedDynamicCache._quantize_component``, mla_quant/cache.py:802-816),
+so passing an instance as that cache's ``quantizer`` runs the evaluation's QDQ
+through these kernels.
 """
 
 from __future__ import annotations
@@ -22,6 +30,7 @@ from __future__ import annotations
 import torch
 
 from . import kernels
+from .artifacts import Artifact
 from .writer import LM_GAIN, LM_THRESHOLD, SUPPORTED_DIMS
 
 GROUP_SIZE = 128
@@ -68,6 +77,21 @@ def _helpers(dev: torch.device, n: int, D: int, R: int):
     return h
 
 
+def _normalize_mask(mask: torch.Tensor, latent: torch.Tensor) -> torch.Tensor:
+    """``[seq]``, ``[batch, seq]`` or ``latent.shape[:-1]`` (``[batch, 1, seq]``)
+    to ``latent.shape[:-1]`` (mla_quant/quantizer.py:85-99)."""
+    mask = mask.to(device=latent.device, dtype=torch.bool)
+    expected = tuple(latent.shape[:-1])
+    if mask.ndim == 1 and len(expected) > 1:
+        mask = mask.reshape(*[1] * (len(expected) - 1), mask.shape[0])
+    elif mask.ndim == 2 and len(expected) == 3:
+        mask = mask.unsqueeze(1)
+    try:
+        return torch.broadcast_to(mask, expected)
+    except RuntimeError as error:
+        raise ValueError(f"high precision mask shape {tuple(mask.shape)} does not match {expected}") from error
+
+
 def rotate_quantize(latent: torch.Tensor, rotation: torch.Tensor, threshold: float = LM_THRESHOLD,
                     gain: float = LM_GAIN, high_precision_mask: torch.Tensor | None = None,
                     group_size: int = GROUP_SIZE) -> torch.Tensor:
@@ -88,7 +112,7 @@ def rotate_quantize(latent: torch.Tensor, rotation: torch.Tensor, threshold: flo
         raise ValueError("rotation must be a [D, D] FP32 matrix")
     mask = None
     if high_precision_mask is not None:
-        mask = torch.broadcast_to(high_precision_mask.to(device=latent.device, dtype=torch.bool), latent.shape[:-1])
+        mask = _normalize_mask(high_precision_mask, latent)
         if bool(mask.all()):
             return latent
     dev = latent.device
@@ -111,3 +135,74 @@ def rotate_quantize(latent: torch.Tensor, rotation: torch.Tensor, threshold: flo
     if mask is None:
         return restored
     return torch.where(mask.unsqueeze(-1), latent, restored)
+
+
+# quantizer.py:31-35: a gain equal to FP32(1.16) is taken as the float64 1.16
+_FP32_STRETCH = float(torch.tensor(LM_GAIN, dtype=torch.float32))
+
+
+class LearnedRotationQuantizer:
+    """GPU inference quantizer over a RoLaQ artifact (mla_quant/quantizer.py:218-316).
+
+    Same construction checks (through :class:`Artifact`: manifest schema, every
+    layer, SHA-256 of each rotation, orthogonality, parameter ranges), same
+    ``quantize_layer`` contract and ``ValueError`` cases, same call counters
+    and ``high_precision_mask`` handling (the last ``T`` positions of the mask
+    for a ``T``-row append). The latent must be a bf16 GPU tensor -- the
+    model's own dtype on this path. ``validate_config`` checks the model fields
+    the manifest records; the checkpoint fingerprint the reference also
+    compares needs the checkpoint files and is not checked here.
+    """
+
+    def __init__(self, artifact_dir):
+        self.artifact = Artifact(artifact_dir)
+        self.root = self.artifact.root
+        self.manifest = self.artifact.manifest
+        self.family = self.manifest["family"]
+        self.width = self.artifact.width
+        self.group_size = GROUP_SIZE
+        self.rotations = {layer: self.artifact.rotation(layer) for layer in self.artifact.layers}
+        self.params = {layer: self.artifact.quantizer(layer) for layer in self.artifact.layers}
+        self.high_precision_mask: torch.Tensor | None = None
+        self.layer_calls = {str(i): {"prefill": 0, "decode": 0} for i in self.rotations}
+        self.call_count = 0
+        self.element_count = 0
+        self.first_shapes: list[tuple[int, ...]] = []
+
+    def validate_config(self, config) -> None:
+        expected = self.manifest.get("model", {})
+        for key in ("model_type", "num_hidden_layers", "kv_lora_rank", "qk_rope_head_dim"):
+            if key in expected and getattr(config, key, None) != expected[key]:
+                raise ValueError(f"learned artifact model mismatch: {key}")
+
+    def quantize_layer(self, tensor: torch.Tensor, layer_idx: int, component: str) -> torch.Tensor:
+        if component != "nope":
+            raise ValueError("learned rotation quantizes nope only")
+        if tensor.ndim < 2 or tensor.shape[-1] != self.width or not tensor.is_floating_point():
+            raise ValueError("invalid MLA latent shape or dtype")
+        if layer_idx not in self.rotations:
+            raise ValueError(f"missing learned rotation for layer {layer_idx}")
+        phase = "decode" if tensor.shape[-2] == 1 else "prefill"
+        self.layer_calls[str(layer_idx)][phase] += 1
+        self.call_count += 1
+        self.element_count += tensor.numel()
+        if len(self.first_shapes) < 4:
+            self.first_shapes.append(tuple(tensor.shape))
+        t, g = self.params[layer_idx]
+        t, g = float(torch.tensor(t, dtype=torch.float32)), float(torch.tensor(g, dtype=torch.float32))
+        if g == _FP32_STRETCH:
+            g = LM_GAIN
+        mask = self.high_precision_mask
+        if mask is not None and mask.shape[-1] != tensor.shape[-2]:
+            mask = mask[..., -tensor.shape[-2]:]
+        return rotate_quantize(tensor, self.rotations[layer_idx], t, g, high_precision_mask=mask)
+
+    def metadata(self) -> dict:
+        return {
+            "recipe": self.manifest["recipe"],
+            "family": self.family,
+            "rotation_dir": str(self.root),
+            "rotation_hashes": {str(k): v.sha256 for k, v in self.artifact.layers.items()},
+            "components": ["nope"],
+            "backend": "librolaq_mla (HIP, gfx950)",
+        }

@@ -145,3 +145,33 @@ def test_fold_read_rotation_absorbs_the_cache_rotation(tmp_path):
     lhs = rotated.double() @ folded.double().T   # absorbed score against the rotated latent
     rhs = c.double() @ wk.double().T             # un-rotated reference
     assert torch.allclose(lhs, rhs, rtol=0, atol=0.03 * rhs.abs().max().item())
+
+
+def test_gpu_quantizer_checks_before_any_launch(tmp_path):
+    """The GPU inference quantizer's contract (mla_quant/quantizer.py:218-316):
+    construction checks, the ValueError cases of quantize_layer and the config
+    check -- all raised on the host before any kernel would run."""
+    from types import SimpleNamespace
+
+    from mla_kv_quant_amd.qdq import LearnedRotationQuantizer
+
+    root, rots, params = make_artifact(tmp_path, layers=2)
+    q = LearnedRotationQuantizer(root)
+    assert q.width == 256 and set(q.rotations) == {0, 1} and q.params[1] == params[1]
+    x = torch.zeros(1, 4, 256, dtype=torch.bfloat16)
+    with pytest.raises(ValueError, match="nope only"):
+        q.quantize_layer(x, 0, "rope")
+    with pytest.raises(ValueError, match="shape or dtype"):
+        q.quantize_layer(torch.zeros(1, 4, 128, dtype=torch.bfloat16), 0, "nope")
+    with pytest.raises(ValueError, match="shape or dtype"):
+        q.quantize_layer(torch.zeros(1, 4, 256, dtype=torch.int32), 0, "nope")
+    with pytest.raises(ValueError, match="missing learned rotation"):
+        q.quantize_layer(x, 5, "nope")
+    assert q.call_count == 0
+    q.validate_config(SimpleNamespace(**dict(MODEL, num_hidden_layers=2)))
+    with pytest.raises(ValueError, match="kv_lora_rank"):
+        q.validate_config(SimpleNamespace(**dict(MODEL, num_hidden_layers=2, kv_lora_rank=512)))
+    # a tampered rotation file fails its SHA-256 at construction
+    torch.save(torch.eye(256), root / "layer_1.pt")
+    with pytest.raises(ValueError, match="SHA-256"):
+        LearnedRotationQuantizer(root)
