@@ -31,6 +31,9 @@ CASES = [
     ("minicpm3_h16", 256, 32, 16, [19, 300, 901], 1, [1, 2, 7]),
     ("dsv2_h32_tp4", 512, 64, 32, [3, 90, 1025], 64, [2, 4, 9]),
     ("dsv2_h8", 512, 64, 8, [48, 777], 16, [3, 6]),
+    ("dsv3_h128", 512, 64, 128, [37, 600, 1100], 64, [3, 5, 9]),  # eight head groups, XCD renumbering
+    ("dsv2_h20", 512, 64, 20, [5, 333, 800], 32, [2, 4, 6]),       # a partial second head group
+    ("h1", 256, 32, 1, [3, 130, 1000], 1, [1, 2, 5]),               # one head: 15 empty MFMA rows
 ]
 
 
