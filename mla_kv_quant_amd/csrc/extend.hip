@@ -11,9 +11,9 @@
 //
 // Layout of the work: a block takes BM consecutive (token, head) query rows of
 // one sequence (all heads share the keys: MQA) and walks the keys in tiles of
-// 32. Each tile is built in LDS by the whole block -- latent+rope rows for the
-// scores and the latent transposed for the output -- while the previous tile
-// is being consumed, double-buffered. Per wave and tile:
+// 32. Each tile is built in LDS by 256 threads of the block -- key rows
+// [latent | rope] -- while the previous tile is being consumed,
+// double-buffered. Per wave and tile:
 //   S^T[32 keys, RW rows] = K . Q^T   on MFMA 16x16x32 (Q held in registers)
 //   softmax in the log2 domain against a fixed per-row reference (the row's
 //   maximum over the first tile); a block whose scores exceed it by more than
@@ -34,9 +34,13 @@ template <int D, int R>
 struct ExtGeo {
   static constexpr int DR = D + R;
   static constexpr int KSQ = DR / 32;               // K-steps of the score MFMA
-  static constexpr int NBR = D == 256 ? 2 : 1;      // 16-row blocks per wave
+  static constexpr int NBR = 1;                     // 16-row blocks per wave
   static constexpr int RW = 16 * NBR;               // query rows per wave
-  static constexpr int BM = 4 * RW;                 // query rows per block
+  // D = 256: 8 waves, two per SIMD (one wave's softmax and tile build overlap
+  // the other's MFMAs; 16 rows per wave keep it within 256 registers);
+  // D = 512: 4 waves, one per SIMD (the 32 output blocks need the registers)
+  static constexpr int WAVES = D == 256 ? 8 : 4;
+  static constexpr int BM = WAVES * RW;             // query rows per block
   static constexpr int ND = D / 16;                 // output column blocks
   static constexpr int KSTR = 2 * DR + 16;          // bytes per key row in LDS
   static constexpr int KBYTES = kExtKeys * KSTR;
@@ -203,7 +207,7 @@ __device__ __forceinline__ u32x2 read_v_tr(const uint8_t* kb, int kstr, int gq, 
 }
 
 template <int D, int R>
-__global__ __launch_bounds__(256, 1) void extend_kernel(ExtendArgs a) {
+__global__ __launch_bounds__((64 * ExtGeo<D, R>::WAVES), 1) void extend_kernel(ExtendArgs a) {
   using G = ExtGeo<D, R>;
   constexpr int KSQ = G::KSQ, NBR = G::NBR, RW = G::RW, BM = G::BM, ND = G::ND;
   extern __shared__ __attribute__((aligned(16))) uint8_t s_buf[];
@@ -227,7 +231,9 @@ __global__ __launch_bounds__(256, 1) void extend_kernel(ExtendArgs a) {
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int gq = lane >> 4, la = lane & 15;
-  const int kq = tid >> 5, o = tid & 31;  // loader role
+  // loader role: the first 256 threads build the tiles (key quad kq, octet o)
+  const int kq = (tid >> 5) & 7, o = tid & 31;
+  const bool ldr = tid < 256;
 
   // ---- query rows of this wave: Q^T fragments and positions -----------------
   u32x4 qf[NBR][KSQ];
@@ -267,10 +273,12 @@ __global__ __launch_bounds__(256, 1) void extend_kernel(ExtendArgs a) {
 
     TileRaw<D, R> raw;
     int32_t sl[4];
-    lookup_tile<D, R>(a, sl, 0, kq, prefix, kv0, kend);
-    load_tile<D, R, false>(a, raw, sl, 0, kq, o, qo0, prefix, L, req, kend);
-    lookup_tile<D, R>(a, sl, kExtKeys, kq, prefix, kv0, kend);
-    store_tile<D, R, false>(raw, s_buf, kq, o);
+    if (ldr) {
+      lookup_tile<D, R>(a, sl, 0, kq, prefix, kv0, kend);
+      load_tile<D, R, false>(a, raw, sl, 0, kq, o, qo0, prefix, L, req, kend);
+      lookup_tile<D, R>(a, sl, kExtKeys, kq, prefix, kv0, kend);
+      store_tile<D, R, false>(raw, s_buf, kq, o);
+    }
     __syncthreads();
 
     for (int it = 0; it < ntiles; ++it) {
@@ -278,7 +286,7 @@ __global__ __launch_bounds__(256, 1) void extend_kernel(ExtendArgs a) {
       const int k0 = it * kExtKeys;
       // loads of the next tile first: they have this tile's compute to land
       // (its pages were looked up an iteration ago)
-      if (it + 1 < ntiles) {
+      if (ldr && it + 1 < ntiles) {
         if (int2_tile(k0 + kExtKeys)) load_tile<D, R, true>(a, raw, sl, k0 + kExtKeys, kq, o, qo0, prefix, L, req, kend);
         else load_tile<D, R, false>(a, raw, sl, k0 + kExtKeys, kq, o, qo0, prefix, L, req, kend);
         lookup_tile<D, R>(a, sl, k0 + 2 * kExtKeys, kq, prefix, kv0, kend);
@@ -359,7 +367,7 @@ __global__ __launch_bounds__(256, 1) void extend_kernel(ExtendArgs a) {
       }
 
       // ---- next tile into the other buffer (last read before the previous barrier)
-      if (it + 1 < ntiles) {
+      if (ldr && it + 1 < ntiles) {
         if (int2_tile(k0 + kExtKeys)) store_tile<D, R, true>(raw, s_buf + ((it + 1) & 1) * G::BUF, kq, o);
         else store_tile<D, R, false>(raw, s_buf + ((it + 1) & 1) * G::BUF, kq, o);
       }
@@ -410,7 +418,7 @@ hipError_t rolaq_launch_extend(const rolaq::ExtendArgs& a, int D, int R, int max
     const hipError_t e = hipFuncSetAttribute((const void*)extend_kernel<DD, RR>,                        \
                                              hipFuncAttributeMaxDynamicSharedMemorySize, lds);          \
     if (e != hipSuccess) return e;                                                                      \
-    hipLaunchKernelGGL((extend_kernel<DD, RR>), grid, dim3(256), lds, stream, a);                       \
+    hipLaunchKernelGGL((extend_kernel<DD, RR>), grid, dim3(64 * G::WAVES), lds, stream, a);             \
     return hipGetLastError();                                                                           \
   }
   ROLAQ_EXT(256, 32)
