@@ -163,19 +163,30 @@ class DecodeBench:
     def flops_per_layer(self) -> float:
         return float(2 * int(self.lengths.sum()) * self.H * (2 * self.D + self.R))
 
-    def pick_splits(self, candidates, layers_label: str = "") -> int:
+    def splits_for(self, policy):
+        """num_kv_splits per request: an int for all, or ("len", T): one INT2
+        split per T tokens of the request plus the window split (a caller's
+        per-request choice, as SGLang sizes splits by sequence length)."""
+        if isinstance(policy, int):
+            return torch.full((self.B,), policy, dtype=torch.int32, device=self.dev), policy
+        per = np.maximum(1, np.ceil(self.lengths / policy[1]).astype(np.int64)) + 1
+        return torch.from_numpy(per.astype(np.int32)).to(self.dev), int(per.max())
+
+    def pick_splits(self, candidates, layers_label: str = ""):
         best = None
-        for ns in candidates:
-            self.alloc_scratch(ns)
-            self.set_splits(ns)
+        for pol in candidates:
+            ns, mx = self.splits_for(pol)
+            self.alloc_scratch(mx)
+            self.ns = ns
             ms = time_loop(self.step, 2, 1)
-            print(f"[bench] {layers_label}splits={ns}: {ms * 1000 / self.layers:.2f} us/layer", file=sys.stderr,
+            print(f"[bench] {layers_label}splits={pol}: {ms * 1000 / self.layers:.2f} us/layer", file=sys.stderr,
                   flush=True)
             if best is None or ms < best[1]:
-                best = (ns, ms)
-        self.alloc_scratch(best[0])
-        self.set_splits(best[0])
-        return best[0]
+                best = (pol, ms)
+        ns, mx = self.splits_for(best[0])
+        self.alloc_scratch(mx)
+        self.ns = ns
+        return best[0] if isinstance(best[0], int) else f"len/{best[0][1]}"
 
 
 def time_loop(fn, steps: int, warmup: int) -> float:
@@ -409,7 +420,7 @@ def reported_decode_result(args, dev: str, name: str) -> dict:
         lens = np.random.default_rng(3).integers(2048, 8193, size=128)
         db = DecodeBench(layers, dev, B=128, lengths=lens, H=16, D=512, R=64, seed=3)
         workload = "cfg3 decode: batch 128, ragged context U[2048,8192], 16 heads, latent 512, rope 64, page 64 shuffled"
-        cands = [2, 3, 4, 5, 6, 8]
+        cands = [2, 3, 4, 5, 6, 8, ("len", 768), ("len", 1024), ("len", 1536), ("len", 2048)]
     else:
         db = DecodeBench(layers, dev, B=64, lengths=[16384] * 64, H=40, D=256, R=32, seed=4)
         workload = "cfg4a decode: batch 64 x context 16384, 40 heads, latent 256, rope 32, page 64 shuffled"
