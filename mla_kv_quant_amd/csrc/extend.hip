@@ -42,7 +42,7 @@ struct ExtGeo {
   static constexpr int WAVES = D == 256 ? 8 : 4;
   static constexpr int BM = WAVES * RW;             // query rows per block
   static constexpr int ND = D / 16;                 // output column blocks
-  static constexpr int KSTR = 2 * DR + 16;          // bytes per key row in LDS
+  static constexpr int KSTR = 2 * DR + 32;          // bytes per key row in LDS (padding measured: +32 B fastest)
   static constexpr int KBYTES = kExtKeys * KSTR;
   static constexpr int BUF = KBYTES;                // one tile: key rows only
   static constexpr int OPT = D / 256;               // latent octets per loader thread
