@@ -253,6 +253,15 @@ int decode_args(const char* who, const void* q, int64_t q_stride_b, int64_t q_st
   a->req_idx = req_idx;
   a->num_kv_splits = num_kv_splits;
   a->S1 = max_kv_splits + 1;
+  // Two stage-1 blocks share a CU; the one dispatched first runs faster (its
+  // waves win issue arbitration), so when every block is resident at once
+  // (at most two per CU, one head group per sequence) the splits whose blocks
+  // fill the first round -- one block per CU -- get larger tile shares.
+  {
+    const int cus = cu_count();
+    const bool one_group = H <= 16;
+    a->fast_splits = (one_group && B <= cus && (int64_t)B * max_kv_splits <= 2 * (int64_t)cus) ? cus / B : 0;
+  }
   a->B = B;
   a->H = H;
   a->P = P;

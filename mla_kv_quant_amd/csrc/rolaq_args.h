@@ -19,6 +19,9 @@ struct DecodeArgs {
   const int64_t* req_idx;
   const int32_t* num_kv_splits;
   int S1;  // max_kv_splits + 1
+  // leading INT2 splits whose blocks take the first dispatch round (one block
+  // per CU) and get the larger tile shares; 0 = equal shares (set by the host)
+  int fast_splits;
   int B, H, P, W;
   float sm_scale;
   float* logits;  // [B, H, S1, D]
