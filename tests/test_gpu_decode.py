@@ -166,3 +166,24 @@ def test_partials_then_merge_equals_fused_call():
         assert torch.equal(l2[b, :, :k].cpu(), logits[b, :, :k])
         assert torch.equal(s2[b, :, :k].cpu(), lse[b, :, :k])
     assert torch.equal(o2.float().cpu(), out)
+
+
+def test_first_round_tile_shares():
+    """32 requests x 16 splits with max_kv_splits 16: every block is resident
+    (two per CU on the 256-CU MI355X), so the first dispatch round's splits get
+    the larger tile shares. Same oracle bars as the other cases, and the merged
+    LSE over all partials equals the exact one."""
+    D, R, H, P, W = 512, 64, 16, 4, 16
+    lengths = [1200 + 53 * i for i in range(32)]
+    sm_scale = 1.0 / math.sqrt(192)
+    pool, slots, pages, reqs, _ = build_pool(lengths, D, R, P, W, 64, seed=21)
+    gp = pool_to_gpu(pool)
+    q = make_queries(len(lengths), H, D, R, sm_scale, seed=22)
+    out, logits, lse = run_decode(gp, q, slots, pages, lengths, reqs, 64, [16] * 32, 16, P, W, sm_scale)
+    ref64, lse64 = attention.decode(pool, q[..., :D], q[..., D:], slots, lengths, reqs, P, W, sm_scale, D, "fp64")
+    torch.testing.assert_close(out.double(), ref64, rtol=RTOL, atol=ATOL)
+    merged = torch.logsumexp(lse[:, :, :16].double(), dim=-1)
+    torch.testing.assert_close(merged, lse64, rtol=0, atol=2e-3)
+    # the first-round splits (0..7 here) hold more tiles than the others: their
+    # partials are non-neutral, and so are those of the rest
+    assert (lse[:, :, :15] > -1.0e4).all()
