@@ -310,7 +310,8 @@ __global__ __launch_bounds__(kThreads, 2) void decode_stage1(DecodeArgs a) {
   __shared__ __attribute__((aligned(16))) u32x4 s_qs[NG][2][2][64];
   __shared__ __attribute__((aligned(16))) u32x4 s_qr[KR][64];  // rope B operands (bf16)
   __shared__ f32x2 s_qq[NG][16];           // per group and head: Qsum / 2, MFMA scale exponent (bits)
-  __shared__ float s_ml[kPairs][16][2];    // per pair and head: reference max, sum
+  __shared__ float s_ml[kPairs][16][3];    // per pair and head: reference max, sum of each wave
+  __shared__ float s_mt[kPairs][2][16];    // per pair, wave and head: largest score seen
 
   const int nhg = (a.H + 15) / 16;
   // Head groups of one (sequence, split) read the same cache rows. With more
@@ -556,7 +557,10 @@ __global__ __launch_bounds__(kThreads, 2) void decode_stage1(DecodeArgs a) {
 
   // phase 1: scores of tokens 16wh + (0..15), left for the partner in this
   // wave's own (now consumed) rope rows of the tile buffer
-  auto phase1 = [&](int tile, uint8_t* tl) {
+  // pre: the pair's reference is known (every tile but the first of the first
+  // pass), so this wave turns its own 16 tokens' scores into probabilities
+  // here -- each softmax term is computed once per pair -- and leaves those
+  auto phase1 = [&](int tile, uint8_t* tl, bool pre) {
     const int p0 = tile * TILE;
     const int tA = 16 * wh + la;  // A-operand token of this lane
     // All of the query's B operands are read up front: read next to its MFMA,
@@ -625,6 +629,16 @@ __global__ __launch_bounds__(kThreads, 2) void decode_stage1(DecodeArgs a) {
     const int pb = p0 + 16 * wh + 4 * gq;
 #pragma unroll
     for (int j = 0; j < 4; ++j) s[j] = (pb + j >= lo && pb + j < hi) ? s[j] * scale_log2 : kNoRef;
+    if (pre) {
+      float ls = 0.f;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        m_seen = fmaxf(m_seen, s[j]);
+        s[j] = __builtin_amdgcn_exp2f(s[j] - m_ref);  // masked: 2^(-1e30) = 0
+        ls += s[j];
+      }
+      l_lane += ls;  // this wave's own tokens only
+    }
     *reinterpret_cast<f32x4*>(tl + G::OFF_R + 16 * G::RBYTES * wh + 16 * lane) = f32x4{s[0], s[1], s[2], s[3]};
     // params of masked tokens (rows that may never have been written) are
     // zeroed for phase 2, so they contribute exactly 0 whatever they held
@@ -639,17 +653,18 @@ __global__ __launch_bounds__(kThreads, 2) void decode_stage1(DecodeArgs a) {
   auto phase2 = [&](const uint8_t* tl, bool first) {
     const f32x4 x0 = *reinterpret_cast<const f32x4*>(tl + G::OFF_R + 16 * lane);
     const f32x4 x1 = *reinterpret_cast<const f32x4*>(tl + G::OFF_R + 16 * G::RBYTES + 16 * lane);
-    const float s[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};  // tokens tau(gq, i)
-    float lm = fmaxf(fmaxf(fmaxf(s[0], s[1]), fmaxf(s[2], s[3])), fmaxf(fmaxf(s[4], s[5]), fmaxf(s[6], s[7])));
-    m_seen = fmaxf(m_seen, lm);
-    if (first) m_ref = wave_max_over_groups(lm);
-    float p[8], ls = 0.f;
+    // tokens tau(gq, i): probabilities, or (first tile of the first pass)
+    // scores, from which both waves take the reference and the probabilities
+    float p[8] = {x0[0], x0[1], x0[2], x0[3], x1[0], x1[1], x1[2], x1[3]};
+    if (first) {
+      const float lm = fmaxf(fmaxf(fmaxf(p[0], p[1]), fmaxf(p[2], p[3])), fmaxf(fmaxf(p[4], p[5]), fmaxf(p[6], p[7])));
+      m_seen = fmaxf(m_seen, lm);
+      m_ref = wave_max_over_groups(lm);
 #pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      p[i] = __builtin_amdgcn_exp2f(s[i] - m_ref);
-      ls += p[i];
+      for (int i = 0; i < 8; ++i) p[i] = __builtin_amdgcn_exp2f(p[i] - m_ref);
+      // the sum counts this wave's own tokens (the partner counts the others)
+      l_lane += wh == 0 ? (p[0] + p[1]) + (p[2] + p[3]) : (p[4] + p[5]) + (p[6] + p[7]);
     }
-    l_lane += ls;
     // tokens tau(gq, i) = 4gq + i (i < 4), 16 + 4gq + i - 4 (i >= 4)
     float scl[GW][8], zr[GW][8];
     uint32_t co[8][GW];
@@ -735,7 +750,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_stage1(DecodeArgs a) {
         __builtin_amdgcn_s_waitcnt(vmcnt_imm(kDmaW));                              \
       else                                                                         \
         __builtin_amdgcn_s_waitcnt(vmcnt_imm(0));                                  \
-      if (act) phase1(tile0 + kPairs * kk, CUR);                                   \
+      if (act) phase1(tile0 + kPairs * kk, CUR, pass > 0 || kk > 0);              \
       lds_barrier();                                                               \
       if (kk + 3 < nmine) lookup(kk + 3, IXL);                                     \
       if (kk + 2 < nmine) dma(tile0 + kPairs * (kk + 2), IXN, NXT);                \
@@ -751,18 +766,19 @@ __global__ __launch_bounds__(kThreads, 2) void decode_stage1(DecodeArgs a) {
 #undef ROLAQ_STEP
     // a score above the reference by more than the slack: redo with the true max
     const float m_true = wave_max_over_groups(m_seen);
+    if (gq == 0) s_mt[pr][wh][la] = m_true;
     const int redo = __syncthreads_or(pass == 0 && m_true > m_ref + kRefSlack);
     if (!redo) break;
-    m_ref = m_true;
+    m_ref = fmaxf(s_mt[pr][0][la], s_mt[pr][1][la]);  // the pair's largest score
   }
 
   // ---- merge the pairs: unnormalised o, m, l --------------------------------
   const float l_sum = wave_sum_over_groups(l_lane);
 #pragma unroll
   for (int gg = 0; gg < GW; ++gg) zp[gg] = wave_sum_over_groups(zp[gg]);
-  if (wh == 0 && gq == 0) {
-    s_ml[pr][la][0] = m_ref;
-    s_ml[pr][la][1] = l_sum;
+  if (gq == 0) {
+    if (wh == 0) s_ml[pr][la][0] = m_ref;
+    s_ml[pr][la][1 + wh] = l_sum;
   }
   __syncthreads();  // every wave is done with its tile buffers
   float fac[4];
@@ -774,7 +790,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_stage1(DecodeArgs a) {
     for (int w = 0; w < kPairs; ++w) M = fmaxf(M, s_ml[w][h][0]);
     float Ls = 0.f;
 #pragma unroll
-    for (int w = 0; w < kPairs; ++w) Ls += __builtin_amdgcn_exp2f(s_ml[w][h][0] - M) * s_ml[w][h][1];
+    for (int w = 0; w < kPairs; ++w) Ls += __builtin_amdgcn_exp2f(s_ml[w][h][0] - M) * (s_ml[w][h][1] + s_ml[w][h][2]);
     fac[j] = Ls > 0.f ? __builtin_amdgcn_exp2f(s_ml[pr][h][0] - M) / Ls : 0.f;
   }
   // this wave's partial o = ((O - 4 SP) 2^(5-e) - ZP) * fac for its groups, in place
@@ -849,7 +865,7 @@ __global__ __launch_bounds__(kThreads, 2) void decode_stage1(DecodeArgs a) {
     float M = kNoRef;
     for (int w = 0; w < kPairs; ++w) M = fmaxf(M, s_ml[w][h][0]);
     float Ls = 0.f;
-    for (int w = 0; w < kPairs; ++w) Ls += __builtin_amdgcn_exp2f(s_ml[w][h][0] - M) * s_ml[w][h][1];
+    for (int w = 0; w < kPairs; ++w) Ls += __builtin_amdgcn_exp2f(s_ml[w][h][0] - M) * (s_ml[w][h][1] + s_ml[w][h][2]);
     a.lse[((int64_t)b * a.H + h0 + h) * a.S1 + split] = Ls > 0.f ? (M + __log2f(Ls)) * kLn2 : kNeutralLse;
   }
 }
