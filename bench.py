@@ -534,7 +534,7 @@ def main():
     db = DecodeBench(args.layers, dev)
     print(f"[bench] decode caches written for {args.layers} layers in {time.time() - t_setup:.1f}s", file=sys.stderr,
           flush=True)
-    ns_best = db.pick_splits([args.splits] if args.splits else [8, 9, 15, 16, 17, 33])
+    ns_best = db.pick_splits([args.splits] if args.splits else [9, 17, 8, 16, 33])
     ms = time_loop(db.step, args.steps, args.warmup)
     us_layer = ms * 1000.0 / args.layers
     bpl = db.bytes_per_layer()

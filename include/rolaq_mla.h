@@ -14,9 +14,9 @@
  *
  * Cache layout per layer (num_slots token slots, D = kv_lora_rank, R = rope
  * dim, NG = D / 128 quantization groups, P sink + W recent BF16 rows):
- *   codes        uint8  [num_slots, D / 4]  2-bit codes; group g owns the
- *                32-bit words NG*s + g (s = 0..7), element 16s+p of the group
- *                at bits 2p of its word.
+ *   codes        uint8  [num_slots, D / 4]  2-bit codes, LSB first: element
+ *                j of the row at byte j / 4, bits 2 (j % 4) (group g = bytes
+ *                32g .. 32g + 31).
  *   params       fp32   [num_slots, NG, 2]  (scale, zero) per group
  *   rope_buf     bf16   [num_slots, R]
  *   hp_c         bf16   [1 + max_reqs * (P + W), D]  rotated latent of the
@@ -124,21 +124,30 @@ int rolaq_prepare_gf_splits(const int32_t* splits, int32_t* quant, int32_t* merg
  *   kv_indices[kv_indptr[b] + t / page_size] * page_size + t % page_size
  * (page_size a power of two; 1 = SGLang's token-level kv_indices).
  * seq_lens: int64 [B] or NULL (then L_b = kv_indptr[b+1] - kv_indptr[b],
- * page_size must be 1). req_idx: int64 [B] ring-row request index.
+ * page_size must be 1). req_idx: int64 [B] ring-row request index; a request
+ * outside [0, max_reqs) has no ring rows (the writer stores none for it) and
+ * is read entirely from its codes. hp_c must hold 1 + max_reqs * (P + W) rows.
+ * Cache rows are the reference's stored rows: an INT2 row is
+ * bf16((code - zero) * scale) (FP32 arithmetic, then rounded to bf16), a
+ * window row (t < P or t >= L_b - W) the hp_c ring row. Window rows are read
+ * by position, which matches the writer's ring as long as a request's
+ * positions are written in order (SGLang serves RoLaQ with its radix cache
+ * disabled, deployment/serve.py:149).
  * num_kv_splits: int32 [B] requested splits ns_b (1 <= ns_b <= max_kv_splits);
- * positions P <= t < L_b - W are split over max(ns_b - 1, 1) INT2 splits,
- * the window rows (t < P or t >= L_b - W, read from hp_c) form split
- * max(ns_b - 1, 1). Partials (normalised output, natural-log LSE; empty
- * splits 0 / -1e4) go to attn_logits fp32 [B, H, max_kv_splits + 1, D] and
+ * positions P <= t < L_b - W and the window rows are split over
+ * max(ns_b - 1, 1) splits (the window rows go with split 0); split
+ * max(ns_b - 1, 1), the reference's window split, holds the neutral partial.
+ * Partials (normalised output, natural-log LSE; empty splits 0 / -1e4) go to
+ * attn_logits fp32 [B, H, max_kv_splits + 1, D] (16-byte aligned) and
  * attn_lse fp32 [B, H, max_kv_splits + 1]; the merged output to out: bf16
  * [B, H, D] with strides (out_stride_b, out_stride_h), in the rotated frame.
- * Supported shapes: (D, R) = (512, 64) or (256, 32), 1 <= H <= 128 (one block
- * per 16 heads); window P + W <= 32.
+ * Supported shapes: (D, R) = (512, 64) or (256, 32), 1 <= H <= 128; window
+ * P + W <= 32.
  */
 int rolaq_decode_fwd(const void* q, int64_t q_stride_b, int64_t q_stride_h, const uint8_t* codes,
                      const float* params, const void* rope_buf, const void* hp_c,
                      const int32_t* kv_indptr, const int32_t* kv_indices, int page_size,
-                     const int64_t* seq_lens, const int64_t* req_idx,
+                     const int64_t* seq_lens, const int64_t* req_idx, int max_reqs,
                      const int32_t* num_kv_splits, int max_kv_splits, int B, int H, int D, int R,
                      int P, int W, float sm_scale, float* attn_logits, float* attn_lse,
                      void* out, int64_t out_stride_b, int64_t out_stride_h, void* stream);
@@ -153,7 +162,7 @@ int rolaq_decode_fwd(const void* q, int64_t q_stride_b, int64_t q_stride_h, cons
 int rolaq_decode_partials(const void* q, int64_t q_stride_b, int64_t q_stride_h, const uint8_t* codes,
                           const float* params, const void* rope_buf, const void* hp_c,
                           const int32_t* kv_indptr, const int32_t* kv_indices, int page_size,
-                          const int64_t* seq_lens, const int64_t* req_idx,
+                          const int64_t* seq_lens, const int64_t* req_idx, int max_reqs,
                           const int32_t* num_kv_splits, int max_kv_splits, int B, int H, int D,
                           int R, int P, int W, float sm_scale, float* attn_logits, float* attn_lse,
                           void* stream);
@@ -179,7 +188,8 @@ int rolaq_decode_merge(const float* attn_logits, const float* attn_lse, const in
  * of page_size) and the chunk itself, causally. Prefix position t is read as
  * the BF16 window row (hp_c ring row of req_idx[b]) when t < P or
  * t >= prefix_lens[b] + chunk length - W, else dequantized from the INT2 row
- * ((code - zero) * scale, rounded to bf16). Chunk rows are k_chunk: bf16
+ * ((code - zero) * scale, rounded to bf16); a request outside [0, max_reqs)
+ * has no window rows. Chunk rows are k_chunk: bf16
  * [T, D + R] (latent | rope), row stride kc_stride_t.
  * q: bf16 [T, H, D + R] (q_lat | q_rope), strides (q_stride_t, q_stride_h).
  * out: bf16 [T, H, D], strides (out_stride_t, out_stride_h), rotated frame.
@@ -189,7 +199,7 @@ int rolaq_decode_merge(const float* attn_logits, const float* attn_lse, const in
 int rolaq_extend_fwd(const void* q, int64_t q_stride_t, int64_t q_stride_h, const void* k_chunk,
                      int64_t kc_stride_t, const int32_t* qo_indptr, const int32_t* kv_indptr,
                      const int32_t* kv_indices, int page_size, const int64_t* prefix_lens,
-                     const int64_t* req_idx, const uint8_t* codes, const float* params,
+                     const int64_t* req_idx, int max_reqs, const uint8_t* codes, const float* params,
                      const void* rope_buf, const void* hp_c, int B, int H, int D, int R, int P, int W,
                      int max_q_len, float sm_scale, void* out, int64_t out_stride_t,
                      int64_t out_stride_h, void* stream);

@@ -64,7 +64,7 @@ extern "C" {
 
 const char* rolaq_last_error(void) { return g_err; }
 
-int rolaq_abi_version(void) { return 1; }
+int rolaq_abi_version(void) { return 2; }
 
 int rolaq_scatter_pack_rows(const float* x, int64_t x_stride, const int32_t* slots, int64_t n, int D,
                             int group_size, float threshold, double gain, uint8_t* codes, float* params,
@@ -218,8 +218,8 @@ namespace {
 int decode_args(const char* who, const void* q, int64_t q_stride_b, int64_t q_stride_h, const uint8_t* codes,
                 const float* params, const void* rope_buf, const void* hp_c, const int32_t* kv_indptr,
                 const int32_t* kv_indices, int page_size, const int64_t* seq_lens, const int64_t* req_idx,
-                const int32_t* num_kv_splits, int max_kv_splits, int B, int H, int D, int R, int P, int W,
-                float sm_scale, float* attn_logits, float* attn_lse, rolaq::DecodeArgs* a) {
+                int max_reqs, const int32_t* num_kv_splits, int max_kv_splits, int B, int H, int D, int R, int P,
+                int W, float sm_scale, float* attn_logits, float* attn_lse, rolaq::DecodeArgs* a) {
   if (!((D == 512 && R == 64) || (D == 256 && R == 32)))
     return fail(ROLAQ_ERR_INVALID, "%s: (D, R) must be (512, 64) or (256, 32), got (%d, %d)", who, D, R);
   if (H <= 0 || H > kMaxHeads) return fail(ROLAQ_ERR_INVALID, "%s: head count %d outside 1..%d", who, H, kMaxHeads);
@@ -231,6 +231,8 @@ int decode_args(const char* who, const void* q, int64_t q_stride_b, int64_t q_st
   if (!seq_lens && page_size != 1) return fail(ROLAQ_ERR_INVALID, "%s: seq_lens required when page_size > 1", who);
   if (max_kv_splits < 1 || max_kv_splits > 4096) return fail(ROLAQ_ERR_INVALID, "%s: max_kv_splits out of range", who);
   if (P < 0 || W < 0 || P + W > 32) return fail(ROLAQ_ERR_INVALID, "%s: need 0 <= P, W and P + W <= 32", who);
+  if (max_reqs < 0) return fail(ROLAQ_ERR_INVALID, "%s: max_reqs < 0", who);
+  if (!aligned(attn_logits, 16)) return fail(ROLAQ_ERR_INVALID, "%s: attn_logits must be 16-byte aligned", who);
   if (!aligned(q, 16) || q_stride_b % 8 || q_stride_h % 8 || q_stride_h < D + R)
     return fail(ROLAQ_ERR_INVALID, "%s: q must be 16-byte aligned with strides multiple of 8 and q_stride_h >= D+R", who);
   if (!aligned(codes, 16) || !aligned(params, 16) || !aligned(rope_buf, 16) || !aligned(hp_c, 16))
@@ -253,15 +255,7 @@ int decode_args(const char* who, const void* q, int64_t q_stride_b, int64_t q_st
   a->req_idx = req_idx;
   a->num_kv_splits = num_kv_splits;
   a->S1 = max_kv_splits + 1;
-  // Two stage-1 blocks share a CU; the one dispatched first runs faster (its
-  // waves win issue arbitration), so when every block is resident at once
-  // (at most two per CU, one head group per sequence) the splits whose blocks
-  // fill the first round -- one block per CU -- get larger tile shares.
-  {
-    const int cus = cu_count();
-    const bool one_group = H <= 16;
-    a->fast_splits = (one_group && B <= cus && (int64_t)B * max_kv_splits <= 2 * (int64_t)cus) ? cus / B : 0;
-  }
+  a->max_reqs = max_reqs;
   a->B = B;
   a->H = H;
   a->P = P;
@@ -279,15 +273,16 @@ extern "C" {
 int rolaq_decode_fwd(const void* q, int64_t q_stride_b, int64_t q_stride_h, const uint8_t* codes,
                      const float* params, const void* rope_buf, const void* hp_c, const int32_t* kv_indptr,
                      const int32_t* kv_indices, int page_size, const int64_t* seq_lens, const int64_t* req_idx,
-                     const int32_t* num_kv_splits, int max_kv_splits, int B, int H, int D, int R, int P, int W,
+                     int max_reqs, const int32_t* num_kv_splits, int max_kv_splits, int B, int H, int D, int R,
+                     int P, int W,
                      float sm_scale, float* attn_logits, float* attn_lse, void* out, int64_t out_stride_b,
                      int64_t out_stride_h, void* stream) {
   if (B < 0) return fail(ROLAQ_ERR_INVALID, "decode_fwd: B < 0");
   if (B == 0) { g_err[0] = '\0'; return ROLAQ_OK; }
   rolaq::DecodeArgs a;
   const int rc = decode_args("decode_fwd", q, q_stride_b, q_stride_h, codes, params, rope_buf, hp_c, kv_indptr,
-                             kv_indices, page_size, seq_lens, req_idx, num_kv_splits, max_kv_splits, B, H, D, R, P,
-                             W, sm_scale, attn_logits, attn_lse, &a);
+                             kv_indices, page_size, seq_lens, req_idx, max_reqs, num_kv_splits, max_kv_splits, B, H,
+                             D, R, P, W, sm_scale, attn_logits, attn_lse, &a);
   if (rc != ROLAQ_OK) return rc;
   if (!out) return fail(ROLAQ_ERR_INVALID, "decode_fwd: null pointer");
   return hip_status(rolaq_launch_decode(a, D, R, max_kv_splits, static_cast<uint16_t*>(out), out_stride_b,
@@ -298,15 +293,15 @@ int rolaq_decode_fwd(const void* q, int64_t q_stride_b, int64_t q_stride_h, cons
 int rolaq_decode_partials(const void* q, int64_t q_stride_b, int64_t q_stride_h, const uint8_t* codes,
                           const float* params, const void* rope_buf, const void* hp_c, const int32_t* kv_indptr,
                           const int32_t* kv_indices, int page_size, const int64_t* seq_lens,
-                          const int64_t* req_idx, const int32_t* num_kv_splits, int max_kv_splits, int B, int H,
-                          int D, int R, int P, int W, float sm_scale, float* attn_logits, float* attn_lse,
-                          void* stream) {
+                          const int64_t* req_idx, int max_reqs, const int32_t* num_kv_splits, int max_kv_splits,
+                          int B, int H, int D, int R, int P, int W, float sm_scale, float* attn_logits,
+                          float* attn_lse, void* stream) {
   if (B < 0) return fail(ROLAQ_ERR_INVALID, "decode_partials: B < 0");
   if (B == 0) { g_err[0] = '\0'; return ROLAQ_OK; }
   rolaq::DecodeArgs a;
   const int rc = decode_args("decode_partials", q, q_stride_b, q_stride_h, codes, params, rope_buf, hp_c, kv_indptr,
-                             kv_indices, page_size, seq_lens, req_idx, num_kv_splits, max_kv_splits, B, H, D, R, P,
-                             W, sm_scale, attn_logits, attn_lse, &a);
+                             kv_indices, page_size, seq_lens, req_idx, max_reqs, num_kv_splits, max_kv_splits, B, H,
+                             D, R, P, W, sm_scale, attn_logits, attn_lse, &a);
   if (rc != ROLAQ_OK) return rc;
   return hip_status(rolaq_launch_decode(a, D, R, max_kv_splits, nullptr, 0, 0, kStagePartials,
                                         static_cast<hipStream_t>(stream)),
@@ -338,9 +333,9 @@ int rolaq_decode_merge(const float* attn_logits, const float* attn_lse, const in
 int rolaq_extend_fwd(const void* q, int64_t q_stride_t, int64_t q_stride_h, const void* k_chunk,
                      int64_t kc_stride_t, const int32_t* qo_indptr, const int32_t* kv_indptr,
                      const int32_t* kv_indices, int page_size, const int64_t* prefix_lens,
-                     const int64_t* req_idx, const uint8_t* codes, const float* params, const void* rope_buf,
-                     const void* hp_c, int B, int H, int D, int R, int P, int W, int max_q_len, float sm_scale,
-                     void* out, int64_t out_stride_t, int64_t out_stride_h, void* stream) {
+                     const int64_t* req_idx, int max_reqs, const uint8_t* codes, const float* params,
+                     const void* rope_buf, const void* hp_c, int B, int H, int D, int R, int P, int W, int max_q_len,
+                     float sm_scale, void* out, int64_t out_stride_t, int64_t out_stride_h, void* stream) {
   if (B < 0 || max_q_len < 0) return fail(ROLAQ_ERR_INVALID, "extend_fwd: B < 0 or max_q_len < 0");
   if (B == 0 || max_q_len == 0) { g_err[0] = '\0'; return ROLAQ_OK; }
   if (!((D == 256 && R == 32) || (D == 512 && R == 64)))
@@ -352,6 +347,7 @@ int rolaq_extend_fwd(const void* q, int64_t q_stride_t, int64_t q_stride_h, cons
   if (page_size < 1 || (page_size & (page_size - 1)))
     return fail(ROLAQ_ERR_INVALID, "extend_fwd: page_size must be a power of two, got %d", page_size);
   if (P < 0 || W < 0) return fail(ROLAQ_ERR_INVALID, "extend_fwd: negative window");
+  if (max_reqs < 0) return fail(ROLAQ_ERR_INVALID, "extend_fwd: max_reqs < 0");
   if (!aligned(q, 16) || q_stride_t % 8 || q_stride_h % 8 || q_stride_h < D + R)
     return fail(ROLAQ_ERR_INVALID, "extend_fwd: q must be 16-byte aligned with strides multiple of 8 and q_stride_h >= D+R");
   if (!aligned(k_chunk, 16) || kc_stride_t % 8 || kc_stride_t < D + R)
@@ -381,6 +377,7 @@ int rolaq_extend_fwd(const void* q, int64_t q_stride_t, int64_t q_stride_h, cons
   a.H = H;
   a.P = P;
   a.W = W;
+  a.max_reqs = max_reqs;
   a.sm_scale = sm_scale;
   a.out = static_cast<uint16_t*>(out);
   a.o_st = out_stride_t;

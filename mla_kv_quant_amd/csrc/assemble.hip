@@ -36,9 +36,9 @@ __global__ __launch_bounds__(256) void assemble_kernel(AssembleArgs a) {
     if (hr >= 0 && a.owner_of_row[hr] == (int32_t)slot) {
       v = *reinterpret_cast<const u32x4*>(a.hp + (int64_t)hr * D + 8 * ch);
     } else {
-      const int d0 = 8 * ch, g = d0 / 128, e0 = d0 % 128;
-      const uint32_t w = *reinterpret_cast<const uint32_t*>(a.codes + slot * (D / 4) + 4 * (NG * (e0 / 16) + g));
-      const uint32_t bits = w >> (16 * ((e0 / 8) & 1));
+      const int d0 = 8 * ch, g = d0 / 128;
+      // elements d0 .. d0+7: bytes d0/4, d0/4 + 1 of the packed row
+      const uint32_t bits = *reinterpret_cast<const uint16_t*>(a.codes + slot * (D / 4) + d0 / 4);
       const f32x2 p = *reinterpret_cast<const f32x2*>(a.params + slot * 2 * NG + 2 * g);
       float f[8];
 #pragma unroll
@@ -124,9 +124,9 @@ __global__ __launch_bounds__(64 * kAsmRotWaves, 1) void assemble_rot_kernel(Asse
   }
   __syncthreads();
   // ---- gather the rows as bf16 into LDS (rows past n as zeros) --------------------
-  // One item = row r and its 16-byte code chunk j: dwords q = 4j + i hold word
-  // s = q / NG of group g = q % NG, i.e. columns 128 g + 16 s + (0..15); each
-  // dword gives two 16-byte LDS chunks. Few, wide loads per thread keep many
+  // One item = row r and its 16-byte code chunk j: dword q = 4j + i is word q
+  // of the row, columns 16 q + (0..15) of group q / 8; each dword gives two
+  // 16-byte LDS chunks. Few, wide loads per thread keep many
   // in flight.
   constexpr int CCH = D / 64;  // 16-byte code chunks per row
   for (int c = tid; c < kAsmRotRows * CCH; c += NT) {
@@ -137,7 +137,7 @@ __global__ __launch_bounds__(64 * kAsmRotWaves, 1) void assemble_rot_kernel(Asse
     if (slot >= 0 && hr >= 0) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const int q = 4 * j + i, col = 128 * (q % NG) + 16 * (q / NG);
+        const int col = 16 * (4 * j + i);
         v[2 * i] = *reinterpret_cast<const u32x4*>(a.hp + (int64_t)hr * D + col);
         v[2 * i + 1] = *reinterpret_cast<const u32x4*>(a.hp + (int64_t)hr * D + col + 8);
       }
@@ -148,7 +148,7 @@ __global__ __launch_bounds__(64 * kAsmRotWaves, 1) void assemble_rot_kernel(Asse
       for (int g = 0; g < NG; ++g) pr[g] = *reinterpret_cast<const f32x2*>(a.params + slot * 2 * NG + 2 * g);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const f32x2 p = pr[(4 * j + i) % NG];
+        const f32x2 p = pr[(4 * j + i) / 8];
         float f[16];
 #pragma unroll
         for (int e = 0; e < 16; ++e) f[e] = (float((w[i] >> (2 * e)) & 3u) - p.y) * p.x;
@@ -162,7 +162,7 @@ __global__ __launch_bounds__(64 * kAsmRotWaves, 1) void assemble_rot_kernel(Asse
     }
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int q = 4 * j + i, col = 128 * (q % NG) + 16 * (q / NG);
+      const int col = 16 * (4 * j + i);
       *reinterpret_cast<u32x4*>(s_x + r * STR + 2 * col) = v[2 * i];
       *reinterpret_cast<u32x4*>(s_x + r * STR + 2 * col + 16) = v[2 * i + 1];
     }

@@ -95,9 +95,9 @@ __device__ __forceinline__ void load_tile(const ExtendArgs& a, TileRaw<D, R>& t,
                                           int kend) {
   constexpr int NG = D / 128, OPT = ExtGeo<D, R>::OPT;
   const int dlo = 8 * OPT * o;  // first latent column of this thread
-  const int g = dlo / 128, e0 = dlo % 128;
+  const int g = dlo / 128;
   if constexpr (INT2) {
-    const uint32_t coff = 4 * (NG * (e0 / 16) + g) + (OPT == 2 ? 0 : 2 * ((e0 / 8) & 1));
+    const uint32_t coff = dlo / 4;  // elements dlo .. of the packed row start at byte dlo / 4
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       const int kp = k0 + 4 * kq + k;
@@ -137,7 +137,7 @@ __device__ __forceinline__ void load_tile(const ExtendArgs& a, TileRaw<D, R>& t,
       rope[k] = a.rope + slot * R + 8 * o;
       mode |= 1u << (2 * k);
     } else {  // INT2 row
-      code[k] = a.codes + slot * (D / 4) + 4 * (NG * (e0 / 16) + g) + (OPT == 2 ? 0 : 2 * ((e0 / 8) & 1));
+      code[k] = a.codes + slot * (D / 4) + dlo / 4;
       prm[k] = a.params + slot * 2 * NG + 2 * g;
       rope[k] = a.rope + slot * R + 8 * o;
       mode |= 2u << (2 * k);
@@ -222,6 +222,9 @@ __global__ __launch_bounds__((64 * ExtGeo<D, R>::WAVES), 1) void extend_kernel(E
   const int64_t prefix = a.prefix_lens[b];
   const int64_t L = prefix + Tq;
   const int64_t req = a.req_idx[b];
+  // a request without ring rows (index outside [0, max_reqs)) has no BF16
+  // window: the writer stored none for it, so its prefix is read from the codes
+  if (req < 0 || req >= a.max_reqs) a.P = a.W = 0;
   const int64_t kv0 = a.kv_indptr[b];
   // last query token of the block -> keys 0 .. prefix + t_last
   const int64_t t_last = min(nrows - 1, r0 + BM - 1) / a.H;

@@ -73,9 +73,8 @@ __global__ __launch_bounds__(256) void pack_rows_kernel(const T* __restrict__ x,
     const uint32_t c = uint32_t(nrm >= -thr) + uint32_t(nrm >= 0.f) + uint32_t(nrm >= thr);
     bits |= c << (2 * i);
   }
-  // element e0+i of group g: word s = e0/16, code p = e0%16 + i -> half (e0/8)&1
-  const int s_word = e0 / 16, half = (e0 / 8) & 1;
-  uint16_t* dst = reinterpret_cast<uint16_t*>(codes + slot * (D / 4) + 4 * (NG * s_word + g)) + half;
+  // elements 8l .. 8l+7 of the row: bytes 2l, 2l+1 (element j at byte j/4, bits 2(j%4))
+  uint16_t* dst = reinterpret_cast<uint16_t*>(codes + slot * (D / 4)) + l;
   *dst = uint16_t(bits);
   if ((l & 15) == 0) {
     const float scale = kscale * std_;

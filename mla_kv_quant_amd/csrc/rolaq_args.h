@@ -18,10 +18,8 @@ struct DecodeArgs {
   const int64_t* seq_lens;
   const int64_t* req_idx;
   const int32_t* num_kv_splits;
-  int S1;  // max_kv_splits + 1
-  // leading INT2 splits whose blocks take the first dispatch round (one block
-  // per CU) and get the larger tile shares; 0 = equal shares (set by the host)
-  int fast_splits;
+  int S1;        // max_kv_splits + 1
+  int max_reqs;  // requests with ring rows; req_idx outside [0, max_reqs) reads no window rows
   int B, H, P, W;
   float sm_scale;
   float* logits;  // [B, H, S1, D]
@@ -87,6 +85,7 @@ struct ExtendArgs {
   const uint16_t* rope;
   const uint16_t* hp;
   int B, H, P, W;
+  int max_reqs;             // req_idx outside [0, max_reqs) reads no window rows
   float sm_scale;
   uint16_t* out;            // [T, H, D] bf16, strides (o_st, o_sh)
   int64_t o_st, o_sh;

@@ -332,9 +332,8 @@ __global__ __launch_bounds__(64 * kWriterWaves, 1) void writer_kernel(WriterArgs
           word[mb >> 2] |= uint32_t(c) << (2 * (4 * (mb & 3) + i));
         }
       if (live) {
-        uint32_t* crow = reinterpret_cast<uint32_t*>(a.codes + sl * (D / 4));
-        crow[NG * (2 * gq) + g] = word[0];
-        crow[NG * (2 * gq + 1) + g] = word[1];
+        // words 2gq, 2gq+1 of group g: row words 8g + 2gq, 8g + 2gq + 1
+        *reinterpret_cast<u32x2*>(a.codes + sl * (D / 4) + 4 * (8 * g + 2 * gq)) = u32x2{word[0], word[1]};
         if (gq == 0) {
           const float scale = a.kscale * std_;
           const float zero = kZeroOffset - mean / scale;

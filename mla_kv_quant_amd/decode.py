@@ -2,8 +2,10 @@
 
 ``prepare_gf_splits`` mirrors deployment/patches/rolaq_sglang.patch:81-92 and
 ``packed_mla_decode_gf_fwd`` the packed decode reader its call site drives
-(rolaq_sglang.patch:51-111): quantized stage 1 over ``max(ns - 1, 1)`` splits,
-one BF16-window split, LSE merge, output in the rotated latent frame.
+(rolaq_sglang.patch:51-111): stage 1 over ``max(ns - 1, 1)`` splits plus the
+window split slot, LSE merge, output in the rotated latent frame. The rows it
+attends over are the reference's stored rows (INT2 rows dequantized and
+rounded to bf16, mla_quant/quantizer.py:120; BF16 window rows).
 """
 
 from __future__ import annotations
@@ -46,4 +48,5 @@ def packed_mla_decode_gf_fwd(q, o, pool, layer_id, kv_indptr, kv_indices, num_kv
             sl = sl.to(torch.int64)
     return kernels.decode_fwd(q, pool.c_codes[li], pool.c_params[li], pool.rope_buf[li], pool.hp_c[li],
                               kv_indptr, kv_indices, sl, req, num_kv_splits, max_kv_splits,
-                              attn_logits, attn_lse, o, sm_scale, P, W, page_size)
+                              attn_logits, attn_lse, o, sm_scale, P, W, page_size,
+                              max_reqs=pool._max_reqs if P + W else 0)

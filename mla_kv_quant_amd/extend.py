@@ -37,4 +37,4 @@ def packed_mla_extend_fwd(q, k, o, pool, layer_id, qo_indptr, kv_indptr, kv_indi
         req = req.to(torch.int64)
     return kernels.extend_fwd(q, k, qo_indptr, kv_indptr, kv_indices, pl, req, pool.c_codes[li], pool.c_params[li],
                               pool.rope_buf[li], pool.hp_c[li], max_q_len, o, sm_scale, pool._win_p, pool._win_r,
-                              page_size)
+                              page_size, max_reqs=pool._max_reqs)

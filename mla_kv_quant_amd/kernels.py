@@ -205,6 +205,20 @@ def _decode_check(q, codes, params, rope_buf, hp_c, kv_indptr, kv_indices, seq_l
     return B, H, D, R
 
 
+def _ring_reqs(hp_c: torch.Tensor, P: int, W: int, max_reqs: int | None) -> int:
+    """Requests whose ring rows ``hp_c`` holds (all of them when not given)."""
+    width = int(P) + int(W)
+    rows = hp_c.shape[0]
+    if max_reqs is None:
+        return (rows - 1) // width if width else 0
+    max_reqs = int(max_reqs)
+    if max_reqs < 0:
+        raise ValueError("max_reqs must be >= 0")
+    if width and rows < 1 + max_reqs * width:
+        raise ValueError(f"hp_c has {rows} rows, fewer than 1 + max_reqs * (P + W) = {1 + max_reqs * width}")
+    return max_reqs
+
+
 def _scratch_check(attn_logits, attn_lse, B, H, D, max_kv_splits, dev):
     S1 = int(max_kv_splits) + 1
     _need(attn_logits, "attn_logits", torch.float32, dev)
@@ -225,14 +239,19 @@ def decode_fwd(q: torch.Tensor, codes: torch.Tensor, params: torch.Tensor, rope_
                hp_c: torch.Tensor, kv_indptr: torch.Tensor, kv_indices: torch.Tensor,
                seq_lens: torch.Tensor | None, req_idx: torch.Tensor, num_kv_splits: torch.Tensor,
                max_kv_splits: int, attn_logits: torch.Tensor, attn_lse: torch.Tensor,
-               out: torch.Tensor, sm_scale: float, P: int, W: int, page_size: int = 1) -> torch.Tensor:
-    """Absorbed decode over the packed cache: ``q [B, H, D+R]`` -> ``out [B, H, D]``."""
+               out: torch.Tensor, sm_scale: float, P: int, W: int, page_size: int = 1,
+               max_reqs: int | None = None) -> torch.Tensor:
+    """Absorbed decode over the packed cache: ``q [B, H, D+R]`` -> ``out [B, H, D]``.
+
+    ``max_reqs``: requests with ring rows in ``hp_c`` (default: as many as its
+    rows hold); a ``req_idx`` outside ``[0, max_reqs)`` reads no window rows."""
     B, H, D, R = _decode_check(q, codes, params, rope_buf, hp_c, kv_indptr, kv_indices, seq_lens, req_idx,
                                num_kv_splits, max_kv_splits, attn_logits, attn_lse)
     _out_check(out, B, H, D, q.device)
+    mr = _ring_reqs(hp_c, P, W, max_reqs)
     _lib.check(_lib.load().rolaq_decode_fwd(
         _p(q), q.stride(0), q.stride(1), _p(codes), _p(params), _p(rope_buf), _p(hp_c),
-        _p(kv_indptr), _p(kv_indices), int(page_size), _p(seq_lens), _p(req_idx), _p(num_kv_splits),
+        _p(kv_indptr), _p(kv_indices), int(page_size), _p(seq_lens), _p(req_idx), mr, _p(num_kv_splits),
         int(max_kv_splits), B, H, D, R, int(P), int(W), float(sm_scale), _p(attn_logits),
         _p(attn_lse), _p(out), out.stride(0), out.stride(1), _stream(q)))
     return out
@@ -242,13 +261,14 @@ def decode_partials(q: torch.Tensor, codes: torch.Tensor, params: torch.Tensor, 
                     hp_c: torch.Tensor, kv_indptr: torch.Tensor, kv_indices: torch.Tensor,
                     seq_lens: torch.Tensor | None, req_idx: torch.Tensor, num_kv_splits: torch.Tensor,
                     max_kv_splits: int, attn_logits: torch.Tensor, attn_lse: torch.Tensor,
-                    sm_scale: float, P: int, W: int, page_size: int = 1) -> None:
+                    sm_scale: float, P: int, W: int, page_size: int = 1, max_reqs: int | None = None) -> None:
     """Stage 1 of :func:`decode_fwd` alone: fills ``attn_logits`` / ``attn_lse``."""
     B, H, D, R = _decode_check(q, codes, params, rope_buf, hp_c, kv_indptr, kv_indices, seq_lens, req_idx,
                                num_kv_splits, max_kv_splits, attn_logits, attn_lse)
+    mr = _ring_reqs(hp_c, P, W, max_reqs)
     _lib.check(_lib.load().rolaq_decode_partials(
         _p(q), q.stride(0), q.stride(1), _p(codes), _p(params), _p(rope_buf), _p(hp_c),
-        _p(kv_indptr), _p(kv_indices), int(page_size), _p(seq_lens), _p(req_idx), _p(num_kv_splits),
+        _p(kv_indptr), _p(kv_indices), int(page_size), _p(seq_lens), _p(req_idx), mr, _p(num_kv_splits),
         int(max_kv_splits), B, H, D, R, int(P), int(W), float(sm_scale), _p(attn_logits),
         _p(attn_lse), _stream(q)))
 
@@ -273,8 +293,11 @@ def decode_merge(attn_logits: torch.Tensor, attn_lse: torch.Tensor, num_kv_split
 def extend_fwd(q: torch.Tensor, k_chunk: torch.Tensor, qo_indptr: torch.Tensor, kv_indptr: torch.Tensor,
                kv_indices: torch.Tensor, prefix_lens: torch.Tensor, req_idx: torch.Tensor, codes: torch.Tensor,
                params: torch.Tensor, rope_buf: torch.Tensor, hp_c: torch.Tensor, max_q_len: int,
-               out: torch.Tensor, sm_scale: float, P: int, W: int, page_size: int = 1) -> torch.Tensor:
-    """Causal extend over the packed prefix + the chunk: ``q [T, H, D+R]`` -> ``out [T, H, D]``."""
+               out: torch.Tensor, sm_scale: float, P: int, W: int, page_size: int = 1,
+               max_reqs: int | None = None) -> torch.Tensor:
+    """Causal extend over the packed prefix + the chunk: ``q [T, H, D+R]`` -> ``out [T, H, D]``.
+
+    ``max_reqs`` as for :func:`decode_fwd`."""
     dev = q.device
     _need(q, "q", torch.bfloat16, dev, 3)
     T, H, DR = q.shape
@@ -304,9 +327,10 @@ def extend_fwd(q: torch.Tensor, k_chunk: torch.Tensor, qo_indptr: torch.Tensor, 
     _need(out, "out", torch.bfloat16, dev, 3)
     if out.shape[0] < T or tuple(out.shape[1:]) != (H, D) or out.stride(2) != 1:
         raise ValueError("out must be [T, H, D] with a contiguous last dim")
+    mr = _ring_reqs(hp_c, P, W, max_reqs)
     _lib.check(_lib.load().rolaq_extend_fwd(
         _p(q), q.stride(0), q.stride(1), _p(k_chunk), k_chunk.stride(0), _p(qo_indptr), _p(kv_indptr),
-        _p(kv_indices), int(page_size), _p(prefix_lens), _p(req_idx), _p(codes), _p(params), _p(rope_buf),
+        _p(kv_indices), int(page_size), _p(prefix_lens), _p(req_idx), mr, _p(codes), _p(params), _p(rope_buf),
         _p(hp_c), B, H, D, R, int(P), int(W), int(max_q_len), float(sm_scale), _p(out), out.stride(0),
         out.stride(1), _stream(q)))
     return out

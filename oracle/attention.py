@@ -41,13 +41,17 @@ def float_to_bf16_bits(x: torch.Tensor) -> np.ndarray:
 
 
 def gather_rows(pool: dict, slots, req: int, length: int, P: int, W: int,
-                width: int, round_bf16: bool = True):
+                width: int, round_bf16: bool = True, max_reqs: int | None = None):
     """Cache rows of one sequence (positions ``0 .. length-1``) as FP32.
 
     Quantized positions are dequantized from ``codes/params`` (optionally
     rounded to bf16, as the reference's QDQ output is); window positions read
-    ``hp`` at their ring row. Returns ``(latent [L, D], rope [L, R])``.
+    ``hp`` at their ring row. A request outside ``[0, max_reqs)`` has no ring
+    rows (the writer keeps none for it, ``mla_fused_writer.py:41``), so all
+    its positions are dequantized. Returns ``(latent [L, D], rope [L, R])``.
     """
+    if max_reqs is not None and not 0 <= int(req) < int(max_reqs):
+        P = W = 0
     slots = np.asarray(slots, dtype=np.int64)[:length]
     pos = np.arange(length)
     codes = layout.unpack_codes(pool["codes"][slots], width)
@@ -93,28 +97,34 @@ def attend_bf16_eager(q_lat, q_rope, k_lat, k_rope, sm_scale: float, mask=None):
 
 
 def decode(pool: dict, q_lat, q_rope, slots_per_seq, lengths, reqs, P: int, W: int,
-           sm_scale: float, width: int, flavour: str = "fp32"):
+           sm_scale: float, width: int, flavour: str = "fp32", max_reqs: int | None = None,
+           batch_index=None):
     """Decode attention for a batch (one query token per sequence).
 
-    ``flavour``: ``"fp64"`` (exact FP32 dequant, float64 arithmetic),
-    ``"fp32"`` (bf16-rounded cache rows, FP32 logits/softmax) or
-    ``"bf16_eager"`` (transformers eager numerics). Returns ``[B, H, D]`` FP32
-    and the natural-log LSE ``[B, H]`` (nan for ``bf16_eager``).
+    ``flavour``: ``"stored64"`` (the reference's stored rows: INT2 rows
+    dequantized in FP32 and rounded to bf16, window rows as stored; float64
+    arithmetic), ``"fp32"`` (the same rows, FP32 logits/softmax), ``"fp64"``
+    (exact FP32 dequant without the bf16 rounding, float64) or
+    ``"bf16_eager"`` (transformers eager numerics). Returns ``[B, H, D]`` and
+    the natural-log LSE ``[B, H]`` (nan for ``bf16_eager``), float64 for the
+    float64 flavours. ``batch_index``: evaluate only these sequences (others
+    stay zero).
     """
     B, H, _ = q_lat.shape
-    out = torch.zeros(B, H, width, dtype=torch.float64 if flavour == "fp64" else torch.float32)
+    wide = flavour in ("fp64", "stored64")
+    out = torch.zeros(B, H, width, dtype=torch.float64 if wide else torch.float32)
     lses = torch.full((B, H), float("nan"), dtype=out.dtype)
-    for b in range(B):
+    for b in (range(B) if batch_index is None else batch_index):
         L = int(lengths[b])
         if L == 0:
             continue
         k_lat, k_rope = gather_rows(pool, slots_per_seq[b], int(reqs[b]), L, P, W, width,
-                                    round_bf16=(flavour != "fp64"))
+                                    round_bf16=(flavour != "fp64"), max_reqs=max_reqs)
         ql, qr = q_lat[b:b + 1].float(), q_rope[b:b + 1].float()
         if flavour == "bf16_eager":
             out[b] = attend_bf16_eager(ql, qr, k_lat, k_rope, sm_scale)[0].float()
         else:
-            dt = torch.float64 if flavour == "fp64" else torch.float32
+            dt = torch.float64 if wide else torch.float32
             o, lse = attend(ql, qr, k_lat, k_rope, sm_scale, dt)
             out[b], lses[b] = o[0].to(out.dtype), lse[0].to(out.dtype)
     return out, lses
@@ -149,15 +159,18 @@ def split_partials(q_lat, q_rope, k_lat, k_rope, sm_scale: float, bounds, dtype=
 def extend(pool: dict, q_lat, q_rope, chunk_lat, chunk_rope, prefix_slots, prefix_len: int,
            req: int, P: int, W: int, sm_scale: float, width: int, chunk_mode: str = "bf16",
            rotation=None, threshold: float = codec.LLOYD_MAX_THRESHOLD,
-           gain: float = codec.LLOYD_MAX_STRETCH, dtype=torch.float32):
+           gain: float = codec.LLOYD_MAX_STRETCH, dtype=torch.float32, max_reqs: int | None = None):
     """Causal extend attention of one sequence: ``Tq`` new queries at positions
-    ``prefix_len ..`` over the packed prefix plus the chunk itself.
+    ``prefix_len ..`` over the packed prefix plus the chunk itself. A request
+    outside ``[0, max_reqs)`` has no window rows (``P = W = 0``).
 
     ``chunk_mode="bf16"`` (SGLang extend semantics, rolaq_sglang.patch:208-235):
     the chunk's own rows enter as the given BF16 rotated latent.
     ``chunk_mode="qdq"`` (HF semantics, cache.py:1030-1039): chunk rows outside
     the last ``W`` positions are Lloyd-QDQ'd (rounded to bf16) before attention.
     """
+    if max_reqs is not None and not 0 <= int(req) < int(max_reqs):
+        P = W = 0
     Tq = q_lat.shape[0]
     L = prefix_len + Tq
     lat_p, rope_p = gather_rows(pool, prefix_slots, req, prefix_len, P, W, width)

@@ -7,18 +7,19 @@ byte (``PF = 8 // bits``, ``MASK = 3``), ``D // group_size`` groups with FP32
 ``(scale, zero)`` each, one row per token slot
 (``deployment/patches/rolaq_sglang.patch:26-34``,
 ``deployment/sglang/QuantKernel/mla_fused_writer.py:86-106``). The bit order
-inside the row lives in an un-vendored SGLang fork, so this build defines it:
+inside the row lives in an un-vendored SGLang fork, so this build defines it
+as the natural LSB-first packing:
 
-* A row of ``D`` codes is ``D / 16`` little-endian 32-bit words of 16 codes.
-* Group ``g`` (``NG = D / 128`` groups) owns the words ``NG * s + g`` for
-  ``s = 0 .. 7``; word ``s`` of group ``g`` holds the group's elements
-  ``16 s .. 16 s + 15``.
-* Element ``16 s + p`` sits at bits ``2p, 2p + 1`` of its word (LSB first).
+* element ``j`` of the row sits at byte ``j >> 2``, bits ``2 (j & 3)`` and
+  ``2 (j & 3) + 1``;
+* equivalently, the row is ``D / 16`` little-endian 32-bit words of 16 codes,
+  group ``g`` (``NG = D / 128``) owns the eight consecutive words
+  ``8 g .. 8 g + 7`` (32 bytes), word ``8 g + s`` holds the group's elements
+  ``16 s .. 16 s + 15`` with element ``16 s + p`` at bits ``2p, 2p + 1``.
 
-Equivalently: the natural LSB-first packing of the row with its 32-bit words
-reordered from (group, word) to (word, group). Every word holds one group
-only, and the 16 bytes ``16 s .. 16 s + 15`` (D = 512) hold word ``s`` of all
-four groups; the decode reader relies on both properties.
+Every word holds one group only, and one group's codes are 32 contiguous
+bytes; the decode reader relies on both properties (a lane loads its group's
+32 bytes with two 16-byte loads and applies one ``(scale, zero)`` to them).
 
 ``params[slot, g] = (scale, zero)`` in FP32, i.e. ``[num_slots, NG, 2]``.
 """
@@ -29,22 +30,23 @@ import numpy as np
 
 GROUP_SIZE = 128
 CODES_PER_WORD = 16
+WORDS_PER_GROUP = GROUP_SIZE // CODES_PER_WORD
 
 
-def word_index(group: int, s: int, num_groups: int) -> int:
+def word_index(group: int, s: int) -> int:
     """Index of word ``s`` of group ``group`` inside a row."""
-    return num_groups * s + group
+    return WORDS_PER_GROUP * group + s
 
 
 def element_position(j: np.ndarray | int, width: int):
-    """Return ``(byte, bit)`` of row element ``j`` (vectorised)."""
+    """Return ``(byte, bit)`` of row element ``j`` (vectorised), computed
+    through the (group, word, code) decomposition."""
     j = np.asarray(j)
-    ng = width // GROUP_SIZE
     g = j // GROUP_SIZE
     f = j % GROUP_SIZE
     s = f // CODES_PER_WORD
     p = f % CODES_PER_WORD
-    w = ng * s + g
+    w = word_index(g, s)
     return 4 * w + p // 4, 2 * (p % 4)
 
 
@@ -58,12 +60,9 @@ def pack_codes(codes: np.ndarray) -> np.ndarray:
         raise ValueError("width must be a multiple of 128")
     if codes.size and int(codes.max()) > 3:
         raise ValueError("codes must be 2-bit")
-    ng = width // GROUP_SIZE
-    c = codes.astype(np.uint32).reshape(rows, ng, GROUP_SIZE // CODES_PER_WORD, CODES_PER_WORD)
-    shifts = (2 * np.arange(CODES_PER_WORD, dtype=np.uint32))
-    words_gs = (c << shifts).sum(axis=-1, dtype=np.uint64).astype(np.uint32)  # [rows, g, s]
-    words = np.ascontiguousarray(words_gs.transpose(0, 2, 1)).reshape(rows, -1)  # [rows, s*ng+g]
-    return words.astype("<u4").view(np.uint8).reshape(rows, width // 4)
+    c = codes.astype(np.uint8).reshape(rows, width // 4, 4)
+    shifts = (2 * np.arange(4, dtype=np.uint8))
+    return np.bitwise_or.reduce(c << shifts, axis=-1).astype(np.uint8)
 
 
 def unpack_codes(packed: np.ndarray, width: int) -> np.ndarray:
@@ -72,16 +71,15 @@ def unpack_codes(packed: np.ndarray, width: int) -> np.ndarray:
     rows = packed.shape[0]
     if packed.shape[1] * 4 != width:
         raise ValueError("packed row length does not match the width")
-    ng = width // GROUP_SIZE
-    words = packed.view("<u4").reshape(rows, GROUP_SIZE // CODES_PER_WORD, ng)  # [rows, s, g]
-    words = words.transpose(0, 2, 1)  # [rows, g, s]
-    shifts = (2 * np.arange(CODES_PER_WORD, dtype=np.uint32))
-    codes = (words[..., None].astype(np.uint32) >> shifts) & 3
+    shifts = (2 * np.arange(4, dtype=np.uint8))
+    codes = (packed[..., None] >> shifts) & 3
     return codes.reshape(rows, width).astype(np.uint8)
 
 
 def pack_codes_bitwise(codes: np.ndarray) -> np.ndarray:
-    """Independent element-by-element packer used to pin :func:`pack_codes`."""
+    """Independent element-by-element packer used to pin :func:`pack_codes`:
+    goes through :func:`element_position` (group / word / code) one element at
+    a time."""
     codes = np.asarray(codes, dtype=np.uint8)
     rows, width = codes.shape
     out = np.zeros((rows, width // 4), dtype=np.uint8)

@@ -77,3 +77,56 @@ def make_queries(B, H, D, R, sm_scale, seed, logit_std=2.0):
 
 def bf16_np_to_torch(a: np.ndarray) -> torch.Tensor:
     return torch.from_numpy(np.ascontiguousarray(a).view(np.int16)).view(torch.bfloat16)
+
+
+def gpu_pool_to_oracle(gp: dict) -> dict:
+    """Host copy of a GPU pool in the oracle's dict format (bf16 as uint16 bits)."""
+    def bits(t):
+        return t.contiguous().view(torch.int16).cpu().numpy().view(np.uint16)
+
+    return {
+        "codes": gp["codes"].cpu().numpy(),
+        "params": gp["params"].cpu().numpy(),
+        "rope": bits(gp["rope"]),
+        "hp": bits(gp["hp"]),
+        "row_of_slot": gp["row_of_slot"].cpu().numpy(),
+        "owner_of_row": gp["owner_of_row"].cpu().numpy(),
+    }
+
+
+def gpu_written_pool(lengths, D, R, P, W, page, seed, max_reqs=None, reqs=None, outliers=None,
+                     device="cuda"):
+    """A pool holding ``len(lengths)`` sequences written as prefills by the
+    library's fused writer (used for sizes where the CPU oracle writer is too
+    slow; the writer itself is held to the oracle in test_gpu_writer.py).
+    Returns (gpu dict, slots per sequence, pages per sequence, request indices)."""
+    from mla_kv_quant_amd import kernels
+
+    B = len(lengths)
+    max_reqs = max_reqs or B + 1
+    reqs = np.asarray(reqs if reqs is not None else np.arange(B) + 1, dtype=np.int64)
+    slots, pages, num_slots = alloc_slots(lengths, page, seed)
+    hp_rows = 1 + max_reqs * (P + W)
+    gp = {
+        "codes": torch.zeros(num_slots, D // 4, dtype=torch.uint8, device=device),
+        "params": torch.zeros(num_slots, D // 128, 2, dtype=torch.float32, device=device),
+        "rope": torch.zeros(num_slots, R, dtype=torch.bfloat16, device=device),
+        "hp": torch.zeros(hp_rows, D, dtype=torch.bfloat16, device=device),
+        "row_of_slot": torch.full((num_slots,), -1, dtype=torch.int32, device=device),
+        "owner_of_row": torch.zeros(hp_rows, dtype=torch.int32, device=device),
+    }
+    rt = synth.make_rotation(D, seed + 17).to(torch.bfloat16).t().contiguous().to(device)
+    live = [b for b in range(B) if lengths[b] > 0]
+    n = int(sum(lengths))
+    if n:
+        loc = torch.from_numpy(np.concatenate([slots[b] for b in live])).to(device)
+        pos = torch.from_numpy(np.concatenate([np.arange(lengths[b]) for b in live])).to(device)
+        seq = torch.from_numpy(np.concatenate([np.full(lengths[b], lengths[b]) for b in live])).to(device)
+        rq = torch.from_numpy(np.concatenate([np.full(lengths[b], reqs[b]) for b in live])).to(device)
+        x = synth.make_latent(n, D, outliers if outliers is not None else max(1, D // 100), seed=seed * 31,
+                              device=device)
+        pe = synth.make_normal((n, R), seed * 37, device=device)
+        kernels.write_rows(x, pe, rt, loc, seq, pos, rq, gp["codes"], gp["params"], gp["rope"], gp["hp"],
+                           gp["row_of_slot"], gp["owner_of_row"], P, W, max_reqs, 0.9810652732849121, 1.16)
+        torch.cuda.synchronize()
+    return gp, slots, pages, reqs

@@ -30,7 +30,7 @@ def test_library_exports_every_declared_symbol():
         assert hasattr(lib, name), name
     # every declared symbol has a ctypes signature in the binding
     assert set(declared_symbols()) - {"rolaq_last_error"} <= set(_lib.SIGNATURES)
-    assert lib.rolaq_abi_version() == 1
+    assert lib.rolaq_abi_version() == 2
 
 
 def test_invalid_arguments_are_rejected_before_any_launch():
@@ -50,15 +50,22 @@ def test_invalid_arguments_are_rejected_before_any_launch():
                                       float("nan"), 1.16, ctypes.c_void_p(16), ctypes.c_void_p(16), None)
     assert bad == _lib.ROLAQ_ERR_INVALID
     p = ctypes.c_void_p(256)
-    args = [p, 16 * 576, 576, p, p, p, p, p, p, 3, p, p, p, 8, 4, 16, 512, 64, 4, 16, 0.07, p, p, p, 8192, 512, None]
+    args = [p, 16 * 576, 576, p, p, p, p, p, p, 3, p, p, 4, p, 8, 4, 16, 512, 64, 4, 16, 0.07, p, p, p, 8192, 512,
+            None]
     assert lib.rolaq_decode_fwd(*args) == _lib.ROLAQ_ERR_INVALID  # page_size 3
     assert b"power of two" in lib.rolaq_last_error()
     args[9] = 1
-    args[15] = 129  # more heads than the grid supports
+    args[16] = 129  # more heads than the grid supports
     assert lib.rolaq_decode_fwd(*args) == _lib.ROLAQ_ERR_INVALID
+    args[16] = 16
+    args[12] = -1  # max_reqs
+    assert lib.rolaq_decode_fwd(*args) == _lib.ROLAQ_ERR_INVALID and b"max_reqs" in lib.rolaq_last_error()
+    args[12] = 4
+    args[22] = ctypes.c_void_p(260)  # attn_logits must be 16-byte aligned
+    assert lib.rolaq_decode_fwd(*args) == _lib.ROLAQ_ERR_INVALID and b"aligned" in lib.rolaq_last_error()
+    args[22] = p
     # stage 1 alone takes the same arguments minus the output
-    pargs = args[:21] + [p, p, None]
-    args[15] = 16
+    pargs = args[:22] + [p, p, None]
     pargs[9] = 3
     assert lib.rolaq_decode_partials(*pargs) == _lib.ROLAQ_ERR_INVALID
     assert b"decode_partials" in lib.rolaq_last_error()
@@ -86,10 +93,10 @@ def test_invalid_arguments_are_rejected_before_any_launch():
     bad[15] = 384
     assert lib.rolaq_norm_write_rows(*bad) == _lib.ROLAQ_ERR_INVALID and b"(D, R)" in lib.rolaq_last_error()
     # extend: shape and pointer checks, empty batch is a no-op
-    eargs = [p, 40 * 288, 288, p, 288, p, p, p, 16, p, p, p, p, p, p, 4, 40, 256, 32, 4, 16, 2048, 0.1, p,
+    eargs = [p, 40 * 288, 288, p, 288, p, p, p, 16, p, p, 4, p, p, p, p, 4, 40, 256, 32, 4, 16, 2048, 0.1, p,
              40 * 256, 256, None]
     bad = list(eargs)
-    bad[17], bad[18] = 384, 32
+    bad[18], bad[19] = 384, 32
     assert lib.rolaq_extend_fwd(*bad) == _lib.ROLAQ_ERR_INVALID and b"(D, R)" in lib.rolaq_last_error()
     bad = list(eargs)
     bad[8] = 12
@@ -98,7 +105,10 @@ def test_invalid_arguments_are_rejected_before_any_launch():
     bad[3] = None
     assert lib.rolaq_extend_fwd(*bad) == _lib.ROLAQ_ERR_INVALID
     bad = list(eargs)
-    bad[15] = 0
+    bad[11] = -2
+    assert lib.rolaq_extend_fwd(*bad) == _lib.ROLAQ_ERR_INVALID and b"max_reqs" in lib.rolaq_last_error()
+    bad = list(eargs)
+    bad[16] = 0
     assert lib.rolaq_extend_fwd(*bad) == _lib.ROLAQ_OK
     # assemble: shapes, strides, pointers; n == 0 is a no-op
     aargs = [p, 10, p, p, p, p, p, p, None, 512, 64, p, 576, None]

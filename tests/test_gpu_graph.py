@@ -6,7 +6,9 @@ padded batch: padding rows use slot 0, which must never claim a window row
 batch (rolaq_sglang.patch:62-111). The captured step is replayed over several
 decode steps, with this program's own eager work (new inputs copied into the
 static buffers) between replays; every replay must leave the pool and the
-output exactly as the same step run eagerly on a twin pool.
+output exactly as the same step run eagerly on a twin pool, and the replayed
+outputs of the live rows must match the oracle's dequantize-then-attention over
+the rows the replays wrote (rtol 2e-2 / atol 2e-3).
 """
 
 import math
@@ -15,8 +17,10 @@ import numpy as np
 import pytest
 import torch
 
+from oracle import attention
 from mla_kv_quant_amd import PackedMLAPool, synth, writer
 from mla_kv_quant_amd.decode import packed_mla_decode_gf_fwd, prepare_gf_splits
+from tests.helpers import gpu_pool_to_oracle
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -112,3 +116,15 @@ def test_captured_decode_step_replays_match_eager():
         assert torch.equal(pg.hp_owner_of_row, pe_.hp_owner_of_row)
         # slot 0 (graph padding) never claims a window row
         assert int(pg.hp_row_of_slot[0]) == -1
+        # the replayed outputs of the live rows against the oracle's
+        # dequantize-then-attention over the rows the replays wrote
+        lens = [L + s + 1 for L in lengths0]
+        slots = [np.arange(base[b], base[b] + lens[b]) for b in range(nreq)]
+        for li in range(layers):
+            pool_np = gpu_pool_to_oracle({"codes": pg.c_codes[li], "params": pg.c_params[li], "rope": pg.rope_buf[li],
+                                          "hp": pg.hp_c[li], "row_of_slot": pg.hp_row_of_slot,
+                                          "owner_of_row": pg.hp_owner_of_row})
+            qh = st["q"][li, :nreq].float().cpu()
+            ref, _ = attention.decode(pool_np, qh[..., :D], qh[..., D:], slots, lens, list(range(1, nreq + 1)), P, W,
+                                      sm, D, "stored64", max_reqs=8)
+            torch.testing.assert_close(og[li, :nreq].float().cpu().double(), ref, rtol=2e-2, atol=2e-3)

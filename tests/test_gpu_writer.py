@@ -158,7 +158,7 @@ def test_fused_writer_prefill_then_decode(D, R):
                                  req_pool_indices=torch.arange(1, nb + 1, device=DEV))
         torch.cuda.synchronize()
         ref64, _ = attention.decode(refs[li], q[..., :D], q[..., D:], slots, lens, list(range(1, nb + 1)), P, W, sm,
-                                    D, "fp64")
+                                    D, "stored64", max_reqs=max_reqs)
         # the GPU pool may differ from the oracle's by rare +-1 codes (the budget above)
         torch.testing.assert_close(o.float().cpu().double(), ref64, rtol=2e-2, atol=2e-3)
 

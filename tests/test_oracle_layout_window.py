@@ -24,17 +24,19 @@ def test_pack_hand_vectors():
     c[0, 0], c[0, 5], c[0, 127] = 1, 3, 2
     p = layout.pack_codes(c)[0]
     assert p[0] == 0b01 and p[1] == 0b11 << 2 and p[31] == 0b10 << 6
-    # D = 512: element 128 + 16*2 + 5 is group 1, word 2, code 5 -> word 4*2+1 = 9
+    # D = 512: element 128 + 16*2 + 5 is group 1, word 2, code 5 -> word 8*1+2 = 10,
+    # byte 4*10 + 5//4 = 41, bits 2*(5%4) = 2
     c = np.zeros((1, 512), np.uint8)
     c[0, 128 + 32 + 5] = 3
     p = layout.pack_codes(c)[0]
-    assert np.flatnonzero(p).tolist() == [37] and p[37] == 3 << 2
-    # the 16 bytes 16s .. 16s+15 hold word s of every group
+    assert np.flatnonzero(p).tolist() == [41] and p[41] == 3 << 2
+    # the 32 bytes 32g .. 32g+31 hold group g, little-endian words in element order
     c = np.zeros((1, 512), np.uint8)
-    for g in range(4):
-        c[0, 128 * g + 16 * 3: 128 * g + 16 * 4] = g
+    c[0, 128 * 2: 128 * 3] = 1
     p = layout.pack_codes(c)[0]
-    assert np.flatnonzero(p).min() >= 48 and np.flatnonzero(p).max() < 64
+    assert np.flatnonzero(p).tolist() == list(range(64, 96)) and (p[64:96] == 0b01010101).all()
+    w = layout.pack_codes(np.arange(16, dtype=np.uint8)[None, :].repeat(8, 0).reshape(1, 128) % 4)[0]
+    assert w.view("<u4")[0] == sum((p % 4) << (2 * p) for p in range(16))
     with pytest.raises(ValueError):
         layout.pack_codes(np.full((1, 128), 4, np.uint8))
 
