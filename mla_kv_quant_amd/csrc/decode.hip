@@ -31,8 +31,10 @@
 //   output     O[head, f] += P V on bf16 MFMA with P as a bf16 hi + lo pair
 //              (FP32-level accuracy) and V read transposed out of the wave's
 //              LDS copy of the expanded tile (ds_read_b64_tr_b16).
-// Loads go straight to registers, two tiles ahead; the four waves merge their
-// (max, sum, O) through LDS into one partial per block.
+// The output contraction of a tile runs inside the next tile's expansion
+// (both touch the same LDS elements, old reads before new writes). Loads go
+// straight to registers, one tile ahead; the four waves merge their (max,
+// sum, O) through LDS into one partial per block.
 #include "rolaq_common.h"
 #include "rolaq_args.h"
 
@@ -44,6 +46,8 @@ constexpr int kThreads = 64 * kWaves;
 constexpr int kXcds = 8;                   // accelerator dies (own L2 each) of the MI355X
 constexpr float kNoRef = -1.0e30f;         // masked score / "no score yet" (log2 units)
 constexpr float kRefSlack = 64.f;          // max exp2 argument before a block is redone
+// s_waitcnt immediate (gfx9 encoding) waiting for lgkmcnt == 0 only
+constexpr int kLgkmcnt0 = 0xF | (0x3 << 14) | (0x7 << 4);
 
 template <int D, int R>
 struct DGeo {
@@ -161,7 +165,7 @@ template <int D, int R, int HG>
 __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
   using G = DGeo<D, R>;
   constexpr int KL = G::KL, KR = G::KR, CB = G::CB, CV = G::CV, WPL = G::WPL, ROWB = G::ROWB, NB = G::NB;
-  constexpr int NG = G::NG, NL = G::NL;
+  constexpr int NG = G::NG;
   static_assert(R % 32 == 0 && D % 256 == 0, "unsupported shape");
   static_assert(16 * D * 4 <= G::WBUF, "merge buffer of one wave (one head group at a time)");
 
@@ -268,10 +272,19 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
     }
   };
 
-  // softmax of one tile (scores S, validity of token 16 mb + 4 gq + r) and its
-  // output contraction against the expanded rows in wbuf
-  auto softmax_output = [&](f32x4 (&S)[2][HG], auto valid, bool first) {
-    u32x4 Ph[HG], Pl[HG];
+  // The output contraction of a tile runs during the next tile's expansion:
+  // word step s of tile i + 1 first reads tile i's V^T for N-blocks 4s..4s+3
+  // (LDS elements 64s..64s+63), then writes its own expanded chunks to those
+  // same elements (LDS executes one wave's operations in order), so one buffer
+  // per wave suffices and the reads' latency and the output MFMAs overlap the
+  // expansion's VALU work. Ph / Pl hold the pending tile's probabilities; at
+  // the start of a pass they are zero and the buffer holds finite values
+  // (zeros, or rows of the previous pass), so the first step's contraction
+  // adds exactly 0.
+  u32x4 Ph[HG], Pl[HG];
+
+  // softmax of one tile (scores S, validity of token 16 mb + 4 gq + r) into Ph / Pl
+  auto softmax = [&](f32x4 (&S)[2][HG], auto valid, bool first) {
 #pragma unroll
     for (int hg = 0; hg < HG; ++hg) {
       float x[8];
@@ -298,56 +311,115 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
         Pl[hg][d] = pack_bf16(p[2 * d] - bf16_lo(hv), p[2 * d + 1] - bf16_hi(hv));
       }
     }
+  };
+  auto out_nb = [&](int nb, u32x2 v0, u32x2 v1) {
+    const u32x4 vt = {v0.x, v0.y, v1.x, v1.y};
 #pragma unroll
-    for (int nb = 0; nb < NB; ++nb) {
-      const u32x2 v0 = read_vt<ROWB>(wbuf, gq, la, nb, 0), v1 = read_vt<ROWB>(wbuf, gq, la, nb, 1);
-      const u32x4 vt = {v0.x, v0.y, v1.x, v1.y};
-#pragma unroll
-      for (int hg = 0; hg < HG; ++hg) {
-        O[hg][nb] = mfma16x16x32(Ph[hg], vt, O[hg][nb]);
-        O[hg][nb] = mfma16x16x32(Pl[hg], vt, O[hg][nb]);
-      }
+    for (int hg = 0; hg < HG; ++hg) {
+      O[hg][nb] = mfma16x16x32(Ph[hg], vt, O[hg][nb]);
+      O[hg][nb] = mfma16x16x32(Pl[hg], vt, O[hg][nb]);
     }
-    // the next tile's expanded rows overwrite these: the stores are issued
-    // after the reads above, and LDS executes one wave's operations in order
+  };
+  // LDS addresses as a few per-lane bases plus immediate offsets. The swizzle
+  // only touches the low 3 bits of a 16-byte chunk index, so
+  //   store of K-step j, M-block mb:  wb[mb][j & 1] + 128 (j >> 1)
+  //   V^T read of N-block nb, half h: rb[nb & 3] + 128 (nb >> 2) + 16 ROWB h
+  // (read_vt's address, regrouped).
+  uint8_t* wb[2][2];
+#pragma unroll
+  for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+    for (int jp = 0; jp < 2; ++jp) {
+      const int row = 16 * mb + la;
+      wb[mb][jp] = wbuf + row * ROWB + 16 * ((4 * jp + gq) ^ sw(row));
+    }
+  const uint8_t* rb[4];
+  {
+    const int row = 4 * gq + (la >> 2), sig = (la & 3) >> 1;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) rb[q] = wbuf + row * ROWB + 16 * ((2 * q + sig) ^ sw(row)) + 8 * (la & 1);
+  }
+  auto vt_read = [&](int nb, int h) {
+    typedef short s16x4 __attribute__((ext_vector_type(4)));
+    typedef __attribute__((address_space(3))) s16x4 lds_s16x4;
+    const uint8_t* p = rb[nb & 3] + 128 * (nb >> 2) + 16 * ROWB * h;
+    return __builtin_bit_cast(u32x2, __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_s16x4*)(p)));
+  };
+  // the pending tile's output alone (after a wave's last tile)
+  auto flush = [&]() {
+    __builtin_amdgcn_s_waitcnt(kLgkmcnt0);  // the last tile's stores have landed
     asm volatile("" ::: "memory");
+#pragma unroll
+    for (int nb = 0; nb < NB; ++nb) out_nb(nb, vt_read(nb, 0), vt_read(nb, 1));
   };
 
-  // INT2 tile i: expand, score, write the rows, softmax, output
+  // INT2 tile i: expand, score, write the rows (with the pending tile's
+  // output interleaved), then its softmax becomes the pending one
   auto compute = [&](int i, const TileRegs<D, R>& d, bool first) {
     const int base = kTile * (T0 + kWaves * i);
+    // rope scores first (their operands are then free), then the latent K-steps
     f32x4 S[2][HG];
 #pragma unroll
+    for (int mb = 0; mb < 2; ++mb)
+#pragma unroll
+      for (int hg = 0; hg < HG; ++hg) {
+        S[mb][hg] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int kr = 0; kr < KR; ++kr) S[mb][hg] = mfma16x16x32(d.rope[mb][kr], qR[hg][kr], S[mb][hg]);
+      }
+    Lut t[2];
+#pragma unroll
     for (int mb = 0; mb < 2; ++mb) {
+      const int pos = base + 16 * mb + la;
+      t[mb] = make_lut(d.prm[mb], pos >= lo && pos < hi);
+    }
+    // Word step s: the expansion of step s with its score MFMAs, then the
+    // reads of step s + 1, then the output MFMAs of step s on the reads issued
+    // in the previous step. Step s stores over the elements its reads came
+    // from, so it first waits for them to be complete (they were issued a
+    // step earlier, so the wait is normally free).
+    u32x2 vr[2][4][2];
 #pragma unroll
-      for (int hg = 0; hg < HG; ++hg) S[mb][hg] = f32x4{0.f, 0.f, 0.f, 0.f};
-      const int row = 16 * mb + la, pos = base + row;
-      const Lut t = make_lut(d.prm[mb], pos >= lo && pos < hi);
-      uint8_t* rp = wbuf + row * ROWB;
-      const int swr = sw(row);
+    for (int k = 0; k < 4; ++k)
 #pragma unroll
-      for (int s = 0; s < WPL; ++s) {
+      for (int h = 0; h < 2; ++h) vr[0][k][h] = vt_read(k, h);
+#pragma unroll
+    for (int s = 0; s < WPL; ++s) {
+      u32x2 (&cur)[4][2] = vr[s & 1];
+      u32x2 (&nxt)[4][2] = vr[(s + 1) & 1];
+      __builtin_amdgcn_s_waitcnt(kLgkmcnt0);  // step s's reads are back
+      asm volatile("" ::: "memory");
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb) {
         u32x4 c0, c1;
-        expand_word(d.code[mb][s / 4][s % 4], t, c0, c1);
-        lds_store128(rp + 16 * ((4 * (2 * s) + gq) ^ swr), c0);
-        lds_store128(rp + 16 * ((4 * (2 * s + 1) + gq) ^ swr), c1);
+        expand_word(d.code[mb][s / 4][s % 4], t[mb], c0, c1);
+        lds_store128(wb[mb][0] + 128 * s, c0);  // K-step 2s
+        lds_store128(wb[mb][1] + 128 * s, c1);  // K-step 2s + 1
 #pragma unroll
         for (int hg = 0; hg < HG; ++hg) {
           S[mb][hg] = mfma16x16x32(c0, qB[hg][2 * s], S[mb][hg]);
           S[mb][hg] = mfma16x16x32(c1, qB[hg][2 * s + 1], S[mb][hg]);
         }
       }
+      asm volatile("" ::: "memory");  // step s + 1's reads after step s's stores
+      if (s + 1 < WPL) {
 #pragma unroll
-      for (int kr = 0; kr < KR; ++kr)
+        for (int k = 0; k < 4; ++k)
 #pragma unroll
-        for (int hg = 0; hg < HG; ++hg) S[mb][hg] = mfma16x16x32(d.rope[mb][kr], qR[hg][kr], S[mb][hg]);
+          for (int h = 0; h < 2; ++h) nxt[k][h] = vt_read(4 * (s + 1) + k, h);
+      }
+#pragma unroll
+      for (int k = 0; k < 4; ++k) out_nb(4 * s + k, cur[k][0], cur[k][1]);
+      // one scheduling region per word step (bounded register lifetimes)
+      __builtin_amdgcn_sched_barrier(0);
     }
-    softmax_output(S, [&](int tok) { return base + tok >= lo && base + tok < hi; }, first);
+    softmax(S, [&](int tok) { return base + tok >= lo && base + tok < hi; }, first);
   };
 
   // window tile: rows 0 .. nw-1 are positions [0, n_sink) U [rec_lo, L) read
   // from the ring rows of hp_c (BF16), staged into wave 0's buffer by the
-  // whole block in the expanded layout, then scored from LDS by wave 0
+  // whole block in the expanded layout, then scored from LDS by wave 0 (always
+  // the first tile of wave 0's pass: no output is pending)
   auto win_pos = [&](int i) { return i < n_sink ? i : rec_lo + (i - n_sink); };
   auto stage_window = [&]() {
     constexpr int CPR = D / 8;  // 16-byte chunks of a row in feature order
@@ -399,12 +471,16 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
 #pragma unroll
         for (int hg = 0; hg < HG; ++hg) S[mb][hg] = mfma16x16x32(rp[mb][kr], qR[hg][kr], S[mb][hg]);
     }
-    softmax_output(S, [&](int tok) { return tok < nw; }, first);
+    softmax(S, [&](int tok) { return tok < nw; }, first);
   };
 
+  // this wave's buffer starts as zeros (see the pending-output rule above)
+#pragma unroll
+  for (int k = 0; k < G::WBUF / 1024; ++k) lds_store128(wbuf + 1024 * k + 16 * lane, u32x4{0u, 0u, 0u, 0u});
+
   // ---- passes (the second only when a score outran the reference) ---------------
-  TileRegs<D, R> d0, d1, d2;
-  int32_t pg0[2], pg1[2], pg2[2];
+  TileRegs<D, R> dc, dn;  // tile being computed / tile in flight
+  int32_t pgc[2], pgn[2];  // their pages
   for (int pass = 0; pass < 2; ++pass) {
 #pragma unroll
     for (int hg = 0; hg < HG; ++hg) {
@@ -412,50 +488,50 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
       for (int nb = 0; nb < NB; ++nb) O[hg][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
       m_seen[hg] = kNoRef;
       l_lane[hg] = 0.f;
+      Ph[hg] = Pl[hg] = u32x4{0u, 0u, 0u, 0u};
     }
     // the window rows go to wave 0's buffer before any tile load is issued
     // (the barrier waits for every load in flight)
     u32x4 rp[2][KR];
     if (win_block) {
+      __syncthreads();  // wave 0's buffer is free (zeroed, or done with the last pass)
       stage_window();
       if (win_mine) window_rope(rp);
       __syncthreads();
-    }
-    // pipeline prologue: pages of tiles 0, 1; data of 0, pages of 2, data of 1,
-    // pages of 3. Indices past the last tile repeat it (loads that hit the L2),
-    // so every step issues the same loads and the compiler's waits stay exact.
-    const int nl = n - 1;
-    if (n > 0) {
-      lookup(0, pg0);
-      lookup(min(1, nl), pg1);
-      load(0, pg0, d0);
-      lookup(min(2, nl), pg2);
-      load(min(1, nl), pg1, d1);
-      lookup(min(3, nl), pg0);
     }
     bool first = pass == 0;
     if (win_mine) {
       window_tile(rp, first);
       first = false;
     }
-    // Step i computes tile i from slot i % 3 after loading tile i + 2 into slot
-    // (i + 2) % 3 (tile i - 1's, consumed) and looking up the pages of tile i + 4.
-#define ROLAQ_STEP(II, CUR, NXT, PGN, PGL)                      \
-    {                                                           \
-      const int ii = (II);                                      \
-      load(min(ii + 2, nl), PGN, NXT);                          \
-      lookup(min(ii + 4, nl), PGL);                             \
-      compute(ii, CUR, first);                                  \
-      first = false;                                            \
+    // Tile pipeline: tile i + 1's data is loaded into dn while tile i is
+    // computed from dc, and the pages are looked up a tile before that. The
+    // loop is not unrolled (the copy dc = dn costs 36 moves per tile): with
+    // unrolled register slots the allocator spills, and four independent waves
+    // per CU keep enough bytes in flight with one tile of prefetch each. The
+    // scheduling barriers keep the issue order, so the compiler's counted
+    // waits release tile i while tile i + 1's loads are in flight.
+    const int nl = n - 1;
+    if (n > 0) {
+      lookup(0, pgc);
+      lookup(min(1, nl), pgn);
+      __builtin_amdgcn_sched_barrier(0);
+      load(0, pgc, dn);
+      __builtin_amdgcn_sched_barrier(0);
     }
-    for (int i = 0; i < n; i += 3) {
-      ROLAQ_STEP(i, d0, d2, pg2, pg1)
-      if (i + 1 >= n) break;
-      ROLAQ_STEP(i + 1, d1, d0, pg0, pg2)
-      if (i + 2 >= n) break;
-      ROLAQ_STEP(i + 2, d2, d1, pg1, pg0)
+    for (int i = 0; i < n; ++i) {
+      dc = dn;  // tile i
+      pgc[0] = pgn[0];
+      pgc[1] = pgn[1];
+      __builtin_amdgcn_sched_barrier(0);
+      load(min(i + 1, nl), pgc, dn);
+      __builtin_amdgcn_sched_barrier(0);
+      lookup(min(i + 2, nl), pgn);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(i, dc, first);
+      first = false;
     }
-#undef ROLAQ_STEP
+    flush();
     // a score above the reference by more than the slack: redo with the true maxima
     // (the sums and accumulators of this pass are relative to m_ref, which
     // therefore changes only when the pass is redone)
