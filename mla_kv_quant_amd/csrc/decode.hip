@@ -46,6 +46,8 @@ constexpr int kThreads = 64 * kWaves;
 constexpr int kXcds = 8;                   // accelerator dies (own L2 each) of the MI355X
 constexpr float kNoRef = -1.0e30f;         // masked score / "no score yet" (log2 units)
 constexpr float kRefSlack = 64.f;          // max exp2 argument before a block is redone
+// instruction classes of __builtin_amdgcn_sched_group_barrier
+constexpr int kSchedValu = 0x002, kSchedMfma = 0x008, kSchedDsRead = 0x100, kSchedDsWrite = 0x200;
 // s_waitcnt immediate (gfx9 encoding) waiting for lgkmcnt == 0 only
 constexpr int kLgkmcnt0 = 0xF | (0x3 << 14) | (0x7 << 4);
 
@@ -357,13 +359,17 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
   // output interleaved), then its softmax becomes the pending one
   auto compute = [&](int i, const TileRegs<D, R>& d, bool first) {
     const int base = kTile * (T0 + kWaves * i);
-    // rope scores first (their operands are then free), then the latent K-steps
-    f32x4 S[2][HG];
+    // rope scores first (their operands are then free), then the latent
+    // K-steps; with one head group, even and odd K-steps accumulate apart (two
+    // independent MFMA chains per M-block), summed before the softmax
+    f32x4 S[2][HG], S2[2][HG];
+    f32x4 (&So)[2][HG] = HG == 1 ? S2 : S;
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
       for (int hg = 0; hg < HG; ++hg) {
         S[mb][hg] = f32x4{0.f, 0.f, 0.f, 0.f};
+        S2[mb][hg] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int kr = 0; kr < KR; ++kr) S[mb][hg] = mfma16x16x32(d.rope[mb][kr], qR[hg][kr], S[mb][hg]);
       }
@@ -373,45 +379,67 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
       const int pos = base + 16 * mb + la;
       t[mb] = make_lut(d.prm[mb], pos >= lo && pos < hi);
     }
-    // Word step s: the expansion of step s with its score MFMAs, then the
-    // reads of step s + 1, then the output MFMAs of step s on the reads issued
-    // in the previous step. Step s stores over the elements its reads came
-    // from, so it first waits for them to be complete (they were issued a
-    // step earlier, so the wait is normally free).
+    // Word step s: the expansion of step s, the output MFMAs of step s on the
+    // reads issued in the previous step, the stores of step s, its score
+    // MFMAs, then the reads of step s + 1. Step s stores over the elements its
+    // reads came from, so it first waits for them (issued a step earlier, the
+    // wait is normally free). The scheduling groups interleave the output
+    // MFMAs with the expansion's VALU work, so the matrix core runs while the
+    // VALU expands, and the score MFMAs with the next reads.
     u32x2 vr[2][4][2];
 #pragma unroll
     for (int k = 0; k < 4; ++k)
 #pragma unroll
       for (int h = 0; h < 2; ++h) vr[0][k][h] = vt_read(k, h);
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int s = 0; s < WPL; ++s) {
       u32x2 (&cur)[4][2] = vr[s & 1];
       u32x2 (&nxt)[4][2] = vr[(s + 1) & 1];
       __builtin_amdgcn_s_waitcnt(kLgkmcnt0);  // step s's reads are back
       asm volatile("" ::: "memory");
+      u32x4 c[2][2];
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb) expand_word(d.code[mb][s / 4][s % 4], t[mb], c[mb][0], c[mb][1]);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) out_nb(4 * s + k, cur[k][0], cur[k][1]);
 #pragma unroll
       for (int mb = 0; mb < 2; ++mb) {
-        u32x4 c0, c1;
-        expand_word(d.code[mb][s / 4][s % 4], t[mb], c0, c1);
-        lds_store128(wb[mb][0] + 128 * s, c0);  // K-step 2s
-        lds_store128(wb[mb][1] + 128 * s, c1);  // K-step 2s + 1
+        lds_store128(wb[mb][0] + 128 * s, c[mb][0]);  // K-step 2s
+        lds_store128(wb[mb][1] + 128 * s, c[mb][1]);  // K-step 2s + 1
+      }
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
         for (int hg = 0; hg < HG; ++hg) {
-          S[mb][hg] = mfma16x16x32(c0, qB[hg][2 * s], S[mb][hg]);
-          S[mb][hg] = mfma16x16x32(c1, qB[hg][2 * s + 1], S[mb][hg]);
+          S[mb][hg] = mfma16x16x32(c[mb][0], qB[hg][2 * s], S[mb][hg]);
+          So[mb][hg] = mfma16x16x32(c[mb][1], qB[hg][2 * s + 1], So[mb][hg]);
         }
-      }
-      asm volatile("" ::: "memory");  // step s + 1's reads after step s's stores
       if (s + 1 < WPL) {
 #pragma unroll
         for (int k = 0; k < 4; ++k)
 #pragma unroll
           for (int h = 0; h < 2; ++h) nxt[k][h] = vt_read(4 * (s + 1) + k, h);
       }
+      // issue order: (5 VALU, HG output MFMAs) x 8, the rest of the VALU,
+      // the stores, then (HG score MFMAs, 2 reads) x 4
 #pragma unroll
-      for (int k = 0; k < 4; ++k) out_nb(4 * s + k, cur[k][0], cur[k][1]);
-      // one scheduling region per word step (bounded register lifetimes)
+      for (int k = 0; k < 8; ++k) {
+        __builtin_amdgcn_sched_group_barrier(kSchedValu, 5, 0);
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, HG, 0);
+      }
+      __builtin_amdgcn_sched_group_barrier(kSchedValu, 64, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedDsWrite, 4, 0);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, HG, 0);
+        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
+      }
       __builtin_amdgcn_sched_barrier(0);
+    }
+    if (HG == 1) {
+#pragma unroll
+      for (int mb = 0; mb < 2; ++mb) S[mb][0] += S2[mb][0];
     }
     softmax(S, [&](int tok) { return base + tok >= lo && base + tok < hi; }, first);
   };
