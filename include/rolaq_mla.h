@@ -153,6 +153,28 @@ int rolaq_decode_fwd(const void* q, int64_t q_stride_b, int64_t q_stride_h, cons
                      void* out, int64_t out_stride_b, int64_t out_stride_h, void* stream);
 
 /*
+ * rolaq_decode_fwd without the attn_logits / attn_lse workspace, for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc). No counterpart in the
+ * reference: it exists only for those callers. Same arguments, rules and
+ * results as rolaq_decode_fwd; the partials go to a static per-GPU scratch
+ * array of 32 MiB held by the library until the process ends, so
+ * B * H * (max_kv_splits + 1) * (D + 1) * 4 bytes (plus up to 255 bytes of
+ * alignment) must fit in 32 MiB, else ROLAQ_ERR_INVALID. The call allocates
+ * nothing. Every call on one GPU shares that GPU's array: calls that overlap
+ * on one GPU (other streams, other threads) race, and the array keeps the last
+ * call's partials (no part of it needs clearing: each call writes every
+ * partial it reads).
+ */
+int rolaq_decode_fwd_noalloc(const void* q, int64_t q_stride_b, int64_t q_stride_h, const uint8_t* codes,
+                             const float* params, const void* rope_buf, const void* hp_c,
+                             const int32_t* kv_indptr, const int32_t* kv_indices, int page_size,
+                             const int64_t* seq_lens, const int64_t* req_idx, int max_reqs,
+                             const int32_t* num_kv_splits, int max_kv_splits, int B, int H, int D, int R,
+                             int P, int W, float sm_scale, void* out, int64_t out_stride_b,
+                             int64_t out_stride_h, void* stream);
+
+/*
  * Stage 1 of rolaq_decode_fwd alone: the split partials and their LSE, with
  * the same arguments and rules (no output). Replaces the quantized stage-1
  * grid plus _fwd_hp_window_stage1 of packed_mla_decode_gf_fwd

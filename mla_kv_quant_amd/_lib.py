@@ -34,6 +34,9 @@ SIGNATURES = {
                          c_void_p, c_int, c_void_p, c_void_p, c_int, c_void_p, c_int, c_int, c_int, c_int,
                          c_int, c_int, c_int, c_float, c_void_p, c_void_p, c_void_p, c_int64, c_int64,
                          c_void_p],
+    "rolaq_decode_fwd_noalloc": [c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
+                                 c_void_p, c_int, c_void_p, c_void_p, c_int, c_void_p, c_int, c_int, c_int, c_int,
+                                 c_int, c_int, c_int, c_float, c_void_p, c_int64, c_int64, c_void_p],
     "rolaq_decode_partials": [c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                               c_void_p, c_int, c_void_p, c_void_p, c_int, c_void_p, c_int, c_int, c_int, c_int,
                               c_int, c_int, c_int, c_float, c_void_p, c_void_p, c_void_p],

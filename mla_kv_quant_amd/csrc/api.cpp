@@ -290,6 +290,41 @@ int rolaq_decode_fwd(const void* q, int64_t q_stride_b, int64_t q_stride_h, cons
                     "decode_fwd launch");
 }
 
+int rolaq_decode_fwd_noalloc(const void* q, int64_t q_stride_b, int64_t q_stride_h, const uint8_t* codes,
+                             const float* params, const void* rope_buf, const void* hp_c, const int32_t* kv_indptr,
+                             const int32_t* kv_indices, int page_size, const int64_t* seq_lens,
+                             const int64_t* req_idx, int max_reqs, const int32_t* num_kv_splits, int max_kv_splits,
+                             int B, int H, int D, int R, int P, int W, float sm_scale, void* out,
+                             int64_t out_stride_b, int64_t out_stride_h, void* stream) {
+  if (B < 0) return fail(ROLAQ_ERR_INVALID, "decode_fwd_noalloc: B < 0");
+  if (B == 0) { g_err[0] = '\0'; return ROLAQ_OK; }
+  if (H <= 0 || (D != 512 && D != 256) || max_kv_splits < 1 || max_kv_splits > 4096)
+    return fail(ROLAQ_ERR_INVALID, "decode_fwd_noalloc: invalid H, D or max_kv_splits");
+  // workspace: attn_logits [B, H, S1, D] fp32, then attn_lse [B, H, S1] fp32 at a 256-byte boundary
+  const uint64_t rows = uint64_t(B) * uint64_t(H) * uint64_t(max_kv_splits + 1);
+  const uint64_t logit_bytes = (rows * uint64_t(D) * 4 + 255) / 256 * 256;
+  const uint64_t need = logit_bytes + rows * 4;
+  if (need > kNoAllocScratchBytes)
+    return fail(ROLAQ_ERR_INVALID,
+                "decode_fwd_noalloc: workspace of %llu bytes (B*H*(max_kv_splits+1)*(D+1)*4) exceeds the "
+                "%llu-byte static scratch; use rolaq_decode_fwd with caller-owned attn_logits/attn_lse",
+                (unsigned long long)need, (unsigned long long)kNoAllocScratchBytes);
+  void* ws = nullptr;
+  const int hrc = hip_status(rolaq_noalloc_scratch(&ws), "decode_fwd_noalloc scratch lookup");
+  if (hrc != ROLAQ_OK) return hrc;
+  float* logits = static_cast<float*>(ws);
+  float* lse = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + logit_bytes);
+  rolaq::DecodeArgs a;
+  const int rc = decode_args("decode_fwd_noalloc", q, q_stride_b, q_stride_h, codes, params, rope_buf, hp_c,
+                             kv_indptr, kv_indices, page_size, seq_lens, req_idx, max_reqs, num_kv_splits,
+                             max_kv_splits, B, H, D, R, P, W, sm_scale, logits, lse, &a);
+  if (rc != ROLAQ_OK) return rc;
+  if (!out) return fail(ROLAQ_ERR_INVALID, "decode_fwd_noalloc: null pointer");
+  return hip_status(rolaq_launch_decode(a, D, R, max_kv_splits, static_cast<uint16_t*>(out), out_stride_b,
+                                        out_stride_h, kStagePartials | kStageMerge, static_cast<hipStream_t>(stream)),
+                    "decode_fwd_noalloc launch");
+}
+
 int rolaq_decode_partials(const void* q, int64_t q_stride_b, int64_t q_stride_h, const uint8_t* codes,
                           const float* params, const void* rope_buf, const void* hp_c, const int32_t* kv_indptr,
                           const int32_t* kv_indices, int page_size, const int64_t* seq_lens,

@@ -38,6 +38,8 @@
 #include "rolaq_common.h"
 #include "rolaq_args.h"
 
+#include <mutex>
+
 namespace rolaq {
 
 constexpr int kTile = 32;                  // tokens per tile (two 16-row M-blocks)
@@ -709,4 +711,33 @@ hipError_t rolaq_launch_decode(const rolaq::DecodeArgs& a, int D, int R, int max
       return hipErrorInvalidValue;
   }
   return hipGetLastError();
+}
+
+// ---------------------------------------------------------------------------
+// Workspace of the allocation-free decode entry point: the split partials
+// and their LSE live in this file-scope array, one copy per GPU, held until
+// the process ends. The kernels take its device address, which host code
+// obtains once per device with hipGetSymbolAddress (the array's name is not a
+// device address in host code).
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) uint8_t scratch[kNoAllocScratchBytes];
+
+hipError_t rolaq_noalloc_scratch(void** ptr) {
+  constexpr int kMaxDevices = 64;
+  static std::mutex mu;
+  static void* per_device[kMaxDevices] = {};
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(mu);
+  if (!per_device[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));  // with device dev current
+    if (e != hipSuccess) return e;
+    if (!p) return hipErrorInvalidSymbol;
+    per_device[dev] = p;
+  }
+  *ptr = per_device[dev];
+  return hipSuccess;
 }

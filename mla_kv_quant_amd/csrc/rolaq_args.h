@@ -114,6 +114,10 @@ struct AssembleArgs {
 constexpr int kStagePartials = 1, kStageMerge = 2;
 hipError_t rolaq_launch_decode(const rolaq::DecodeArgs& a, int D, int R, int max_splits, uint16_t* out,
                                int64_t o_sb, int64_t o_sh, int stages, hipStream_t stream);
+// Device address, on the current device, of the allocation-free decode's
+// static workspace of kNoAllocScratchBytes bytes (looked up once per device).
+constexpr size_t kNoAllocScratchBytes = size_t(32) << 20;
+hipError_t rolaq_noalloc_scratch(void** ptr);
 hipError_t rolaq_launch_pack_f32(const float* x, int64_t xs, const int32_t* slots, int64_t n, int D,
                                  float thr, float kscale, uint8_t* codes, float* params, hipStream_t stream);
 hipError_t rolaq_launch_pack_bf16_aux(const uint16_t* x, int64_t xs, const int64_t* loc, int64_t n, int D,
