@@ -78,13 +78,6 @@ __device__ __forceinline__ u32x4 rms_apply8(u32x4 v, float r, u32x4 gm) {
   return o;
 }
 
-// floor(x) as int32 in one instruction (v_cvt_flr_i32_f32; saturates, which
-// the caller's clamp to 0..3 absorbs).
-__device__ __forceinline__ int floor_to_int(float x) {
-  int r;
-  asm("v_cvt_flr_i32_f32 %0, %1" : "=v"(r) : "v"(x));
-  return r;
-}
 
 template <int D>
 struct WriterGeo {
@@ -144,7 +137,6 @@ __global__ __launch_bounds__(64 * kWriterWaves, 1) void writer_kernel(WriterArgs
   }
   __syncthreads();
 
-  const float inv_t = 1.0f / a.thr;
   const int64_t ntiles = (a.n + kWriterRows - 1) / kWriterRows;
   const int64_t tstep = (int64_t)a.nstripes * kWriterWaves;
   const uint8_t* lds_a = s_rt + la * STR + 16 * gq;
@@ -321,15 +313,17 @@ __global__ __launch_bounds__(64 * kWriterWaves, 1) void writer_kernel(WriterArgs
         }
       q = sum_over_rows(q);
       const float std_ = sqrtf(q * (1.0f / 128.0f) + 1e-08f);
-      // code = #{-t, 0, t <= (x - mean) / std} = clamp(floor((x - mean) / (t std) + 2), 0, 3)
-      const float k = (1.0f / std_) * inv_t;
+      // code = #{-t, 0, t <= normalized}, normalized = (x - mean) / std with a
+      // correctly rounded FP32 division (oscar.py:135-140, operation for operation)
+      const float t = a.thr;
       uint32_t word[2] = {0u, 0u};
 #pragma unroll
       for (int mb = 0; mb < 8; ++mb)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const int c = min(max(floor_to_int(fmaf(acc[mb][nb][i], k, 2.0f)), 0), 3);
-          word[mb >> 2] |= uint32_t(c) << (2 * (4 * (mb & 3) + i));
+          const float nrm = acc[mb][nb][i] / std_;
+          const uint32_t c = uint32_t(nrm >= -t) + uint32_t(nrm >= 0.f) + uint32_t(nrm >= t);
+          word[mb >> 2] |= c << (2 * (4 * (mb & 3) + i));
         }
       if (live) {
         // words 2gq, 2gq+1 of group g: row words 8g + 2gq, 8g + 2gq + 1

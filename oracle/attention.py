@@ -159,7 +159,8 @@ def split_partials(q_lat, q_rope, k_lat, k_rope, sm_scale: float, bounds, dtype=
 def extend(pool: dict, q_lat, q_rope, chunk_lat, chunk_rope, prefix_slots, prefix_len: int,
            req: int, P: int, W: int, sm_scale: float, width: int, chunk_mode: str = "bf16",
            rotation=None, threshold: float = codec.LLOYD_MAX_THRESHOLD,
-           gain: float = codec.LLOYD_MAX_STRETCH, dtype=torch.float32, max_reqs: int | None = None):
+           gain: float = codec.LLOYD_MAX_STRETCH, dtype=torch.float32, max_reqs: int | None = None,
+           rows=None):
     """Causal extend attention of one sequence: ``Tq`` new queries at positions
     ``prefix_len ..`` over the packed prefix plus the chunk itself. A request
     outside ``[0, max_reqs)`` has no window rows (``P = W = 0``).
@@ -168,6 +169,7 @@ def extend(pool: dict, q_lat, q_rope, chunk_lat, chunk_rope, prefix_slots, prefi
     the chunk's own rows enter as the given BF16 rotated latent.
     ``chunk_mode="qdq"`` (HF semantics, cache.py:1030-1039): chunk rows outside
     the last ``W`` positions are Lloyd-QDQ'd (rounded to bf16) before attention.
+    ``rows``: evaluate only the queries of these chunk rows (returns ``[len(rows), H, D]``).
     """
     if max_reqs is not None and not 0 <= int(req) < int(max_reqs):
         P = W = 0
@@ -197,6 +199,9 @@ def extend(pool: dict, q_lat, q_rope, chunk_lat, chunk_rope, prefix_slots, prefi
     k_rope = torch.cat([rope_p, chunk_rope.float()], 0)
     qpos = torch.arange(prefix_len, L)[:, None]
     kpos = torch.arange(L)[None, :]
+    if rows is not None:  # only these chunk rows' queries (the keys are the whole chunk's)
+        rows = torch.as_tensor(rows, dtype=torch.long)
+        q_lat, q_rope, qpos = q_lat[rows], q_rope[rows], qpos[rows]
     return attend(q_lat, q_rope, k_lat, k_rope, sm_scale, dtype, mask=kpos <= qpos)
 
 

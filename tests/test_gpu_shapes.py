@@ -1,0 +1,210 @@
+"""GPU parity at the benchmark shapes (the configurations bench.py times).
+
+Each case runs the kernels at the configuration's full size and checks what
+the CPU oracle can evaluate in seconds: every row the writer stores (cfg1),
+and sampled sequences / query rows of the readers (cfg2, cfg3, cfg4a, cfg4b)
+against the reference's dequantize-then-attention over its stored rows
+(``oracle.attention`` "stored64" / float64 extend), rtol 2e-2 / atol 2e-3.
+The readers' caches are written by the library's fused writer (held to the
+oracle row for row in the cfg1 case and in test_gpu_writer.py); the oracle
+reads the same cache bytes.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import attention, layout, window
+from mla_kv_quant_amd import kernels, synth
+from tests.helpers import alloc_slots, bf16_np_to_torch, gpu_pool_to_oracle, gpu_written_pool, index_lists
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+RTOL, ATOL = 2e-2, 2e-3
+THR, GAIN = 0.9810652732849121, 1.16
+
+
+def _decode(gp, q, slots, pages, lengths, reqs, page, splits, max_splits, P, W, sm):
+    B, H, _ = q.shape
+    D = gp["codes"].shape[1] * 4
+    indptr, indices = index_lists(slots, pages, page)
+    out = torch.empty(B, H, D, dtype=torch.bfloat16, device=DEV)
+    logits = torch.empty(B, H, max_splits + 1, D, device=DEV)
+    lse = torch.empty(B, H, max_splits + 1, device=DEV)
+    kernels.decode_fwd(q.to(DEV), gp["codes"], gp["params"], gp["rope"], gp["hp"], indptr, indices,
+                       torch.tensor(lengths, dtype=torch.int64, device=DEV),
+                       torch.tensor(np.asarray(reqs), dtype=torch.int64, device=DEV),
+                       torch.tensor(splits, dtype=torch.int32, device=DEV), max_splits, logits, lse, out, sm, P, W,
+                       page)
+    torch.cuda.synchronize()
+    return out.float().cpu(), lse.cpu()
+
+
+def _check_sampled(pool_np, q, out, lse, slots, lengths, reqs, splits, P, W, sm, D, sample):
+    ref, ref_lse = attention.decode(pool_np, q[..., :D], q[..., D:], slots, lengths, reqs, P, W, sm, D, "stored64",
+                                    batch_index=sample)
+    for b in sample:
+        torch.testing.assert_close(out[b].double(), ref[b], rtol=RTOL, atol=ATOL)
+        nq = max(splits[b] - 1, 1)
+        torch.testing.assert_close(torch.logsumexp(lse[b, :, : nq + 1].double(), -1), ref_lse[b], rtol=0, atol=2e-3)
+
+
+def test_cfg1_writer_serving_shape_flip_rate():
+    """64 sequences x one 2048-token prefill chunk, page 64, s4r16, D=512 / R=64,
+    1% outlier channels x20: every stored row against oracle.window.write_rows.
+    The rotation runs on bf16 MFMA with FP32 accumulation (exact products, another
+    summation order than the oracle's FP32 GEMM), so a code can flip by one level
+    where a normalized value sits within rounding of a threshold; the north star
+    allows <= 1e-5 of elements."""
+    D, R, P, W, page, B, T = 512, 64, 4, 16, 64, 64, 2048
+    max_reqs = B + 1
+    slots, _, num_slots = alloc_slots([T] * B, page, seed=41)
+    loc = np.concatenate(slots)
+    n = B * T
+    pos = np.tile(np.arange(T), B)
+    seq = np.full(n, T)
+    req = np.repeat(np.arange(1, B + 1), T)
+    x = synth.make_latent(n, D, D // 100, seed=5)
+    pe = synth.make_normal((n, R), 6)
+    rot = synth.make_rotation(D, 7)
+    ref = window.new_pool(num_slots, D, R, max_reqs, P, W)
+    window.write_rows(ref, x, pe, loc, seq, req, rot, THR, GAIN, P, W, max_reqs, positions=pos)
+    hp_rows = 1 + max_reqs * (P + W)
+    gp = {
+        "codes": torch.zeros(num_slots, D // 4, dtype=torch.uint8, device=DEV),
+        "params": torch.zeros(num_slots, D // 128, 2, device=DEV),
+        "rope": torch.zeros(num_slots, R, dtype=torch.bfloat16, device=DEV),
+        "hp": torch.zeros(hp_rows, D, dtype=torch.bfloat16, device=DEV),
+        "row_of_slot": torch.full((num_slots,), -1, dtype=torch.int32, device=DEV),
+        "owner_of_row": torch.zeros(hp_rows, dtype=torch.int32, device=DEV),
+    }
+    rt = rot.to(torch.bfloat16).t().contiguous().to(DEV)
+    kernels.write_rows(x.to(DEV), pe.to(DEV), rt, torch.from_numpy(loc).to(DEV), torch.from_numpy(seq).to(DEV),
+                       torch.from_numpy(pos).to(DEV), torch.from_numpy(req).to(DEV), gp["codes"], gp["params"],
+                       gp["rope"], gp["hp"], gp["row_of_slot"], gp["owner_of_row"], P, W, max_reqs, THR, GAIN)
+    torch.cuda.synchronize()
+    got = gpu_pool_to_oracle(gp)
+    gc = layout.unpack_codes(got["codes"][loc], D).astype(np.int16)
+    rc = layout.unpack_codes(ref["codes"][loc], D).astype(np.int16)
+    diff = gc - rc
+    flips = int(np.count_nonzero(diff))
+    rate = flips / diff.size
+    print(f"cfg1 writer: {flips} of {diff.size} codes differ by one level (rate {rate:.2e})")
+    assert np.abs(diff).max(initial=0) <= 1
+    assert rate <= 1e-5
+    torch.testing.assert_close(torch.from_numpy(got["params"][loc][..., 0]),
+                               torch.from_numpy(ref["params"][loc][..., 0]), rtol=1e-5, atol=0)
+    torch.testing.assert_close(torch.from_numpy(got["params"][loc][..., 1]),
+                               torch.from_numpy(ref["params"][loc][..., 1]), rtol=1e-4, atol=1e-4)
+    assert np.array_equal(got["rope"][loc], ref["rope"][loc])
+    torch.testing.assert_close(bf16_np_to_torch(got["hp"]).float(), bf16_np_to_torch(ref["hp"]).float(),
+                               rtol=2 ** -7, atol=1e-6)
+    assert np.array_equal(got["row_of_slot"], ref["row_of_slot"])
+    assert np.array_equal(got["owner_of_row"], ref["owner_of_row"])
+
+
+def test_cfg2_decode_full_shape():
+    """32 x 16384 tokens, 16 heads, page 64, s4r16: per-request split counts
+    1, 2, 9, 16 and the reference's static 129 (serve.py:198) in one batch."""
+    D, R, H, P, W, page, B, L = 512, 64, 16, 4, 16, 64, 32, 16384
+    lengths = [L] * B
+    gp, slots, pages, reqs = gpu_written_pool(lengths, D, R, P, W, page, seed=3)
+    sm = 1.0 / math.sqrt(192)
+    q = synth.make_normal((B, H, D + R), 11, std=2.0 / (sm * math.sqrt(D + R)))
+    splits = [[1, 2, 9, 16, 129][b % 5] for b in range(B)]
+    out, lse = _decode(gp, q, slots, pages, lengths, reqs, page, splits, 129, P, W, sm)
+    assert torch.isfinite(out).all()
+    _check_sampled(gpu_pool_to_oracle(gp), q, out, lse, slots, lengths, reqs, splits, P, W, sm, D,
+                   [0, 1, 2, 3, 4, 31])
+
+
+def test_cfg3_ragged_paged_split_vs_unsplit():
+    """Batch 128, lengths uniform in [2048, 8192], shuffled 64-token pages,
+    ceil(L / 2048) splits per request; sampled requests against the oracle and
+    every request against the unsplit (one split) run."""
+    D, R, H, P, W, page, B = 512, 64, 16, 4, 16, 64, 128
+    lengths = [int(v) for v in np.random.default_rng(8).integers(2048, 8193, B)]
+    gp, slots, pages, reqs = gpu_written_pool(lengths, D, R, P, W, page, seed=8)
+    sm = 1.0 / math.sqrt(192)
+    q = synth.make_normal((B, H, D + R), 12, std=2.0 / (sm * math.sqrt(D + R)))
+    splits = [math.ceil(v / 2048) for v in lengths]
+    out, lse = _decode(gp, q, slots, pages, lengths, reqs, page, splits, 4, P, W, sm)
+    one, _ = _decode(gp, q, slots, pages, lengths, reqs, page, [1] * B, 4, P, W, sm)
+    torch.testing.assert_close(out, one, rtol=2 ** -7, atol=1e-3)
+    _check_sampled(gpu_pool_to_oracle(gp), q, out, lse, slots, lengths, reqs, splits, P, W, sm, D,
+                   [0, 17, 64, 127])
+
+
+def test_cfg4a_decode_full_shape():
+    """MiniCPM3 shape: 64 x 16384 tokens, 40 heads (three head groups of one
+    block), D=256 / R=32, page 64, s4r16."""
+    D, R, H, P, W, page, B, L = 256, 32, 40, 4, 16, 64, 64, 16384
+    lengths = [L] * B
+    gp, slots, pages, reqs = gpu_written_pool(lengths, D, R, P, W, page, seed=4)
+    sm = 1.0 / math.sqrt(96)
+    q = synth.make_normal((B, H, D + R), 13, std=2.0 / (sm * math.sqrt(D + R)))
+    splits = [[5, 2][b % 2] for b in range(B)]
+    out, lse = _decode(gp, q, slots, pages, lengths, reqs, page, splits, 5, P, W, sm)
+    assert torch.isfinite(out).all()
+    _check_sampled(gpu_pool_to_oracle(gp), q, out, lse, slots, lengths, reqs, splits, P, W, sm, D, [0, 1, 63])
+
+
+def test_cfg4b_extend_full_shape():
+    """Batch 4 of 2048 new causal query tokens over a 14336-token INT2 prefix
+    plus the s4r16 window, 40 heads, D=256 / R=32, page 64; 64 sampled query
+    rows per sequence (the first, the last and 62 seeded) against the oracle."""
+    D, R, H, P, W, page, B, prefix, T = 256, 32, 40, 4, 16, 64, 4, 14336, 2048
+    prefixes = [prefix] * B
+    gp, slots, pages, reqs = gpu_written_pool(prefixes, D, R, P, W, page, seed=9)
+    sm = 1.0 / math.sqrt(96)
+    q = synth.make_normal((B * T, H, D + R), 14, std=2.0 / (sm * math.sqrt(D + R)))
+    kc = torch.cat([synth.make_latent(B * T, D, D // 100, seed=15), synth.make_normal((B * T, R), 16)],
+                   1).to(torch.bfloat16)
+    qo = torch.arange(0, (B + 1) * T, T, dtype=torch.int32)
+    indptr, indices = index_lists(slots, pages, page)
+    out = torch.full((B * T, H, D), float("nan"), dtype=torch.bfloat16, device=DEV)
+    kernels.extend_fwd(q.to(DEV), kc.to(DEV), qo.to(DEV), indptr, indices,
+                       torch.tensor(prefixes, dtype=torch.int64, device=DEV),
+                       torch.tensor(np.asarray(reqs), dtype=torch.int64, device=DEV), gp["codes"], gp["params"],
+                       gp["rope"], gp["hp"], T, out, sm, P, W, page)
+    torch.cuda.synchronize()
+    out = out.float().cpu()
+    assert torch.isfinite(out).all()
+    pool_np = gpu_pool_to_oracle(gp)
+    rng = np.random.default_rng(17)
+    for b in range(B):
+        rows = np.unique(np.concatenate([[0, T - 1], rng.integers(0, T, 62)]))
+        s = b * T
+        ref, _ = attention.extend(pool_np, q[s:s + T, :, :D], q[s:s + T, :, D:], kc[s:s + T, :D], kc[s:s + T, D:],
+                                  slots[b], prefix, int(reqs[b]), P, W, sm, D, dtype=torch.float64, rows=rows)
+        torch.testing.assert_close(out[s + rows].double(), ref, rtol=RTOL, atol=ATOL)
+
+
+def test_reused_request_index_reads_the_new_requests_rows():
+    """A request index is reused after its request finished: the new request's
+    prefill overwrites the ring rows (in position order, as SGLang serves RoLaQ
+    with the radix cache disabled, serve.py:149), and decode reads only them."""
+    D, R, H, P, W, page = 512, 64, 16, 4, 16, 16
+    max_reqs = 3
+    # request index 1 first serves a 900-token sequence, then a 300-token one
+    gp, slots, pages, _ = gpu_written_pool([900, 300], D, R, P, W, page, seed=21, max_reqs=max_reqs,
+                                           reqs=[1, 2])
+    old_hp = gp["hp"].clone()
+    from mla_kv_quant_amd import synth as sy
+    rt = sy.make_rotation(D, 21 + 17).to(torch.bfloat16).t().contiguous().to(DEV)
+    L = 300
+    x = sy.make_latent(L, D, 5, seed=77, device=DEV)
+    pe = sy.make_normal((L, R), 78, device=DEV)
+    loc = torch.from_numpy(slots[1]).to(DEV)  # reuse the second sequence's slots for the new request
+    kernels.write_rows(x, pe, rt, loc, torch.full((L,), L, device=DEV), torch.arange(L, device=DEV),
+                       torch.full((L,), 1, device=DEV), gp["codes"], gp["params"], gp["rope"], gp["hp"],
+                       gp["row_of_slot"], gp["owner_of_row"], P, W, max_reqs, THR, GAIN)
+    torch.cuda.synchronize()
+    ring = slice(1 + 1 * (P + W), 1 + 2 * (P + W))
+    assert not torch.equal(gp["hp"][ring], old_hp[ring])  # the old request's rows are gone
+    sm = 1.0 / math.sqrt(192)
+    q = synth.make_normal((1, H, D + R), 19, std=2.0 / (sm * math.sqrt(D + R)))
+    out, lse = _decode(gp, q, [slots[1]], [pages[1]], [L], [1], page, [3], 3, P, W, sm)
+    _check_sampled(gpu_pool_to_oracle(gp), q, out, lse, [slots[1]], [L], [1], [3], P, W, sm, D, [0])
