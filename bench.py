@@ -19,8 +19,10 @@ U[2048, 8192], shuffled pages) and config 4a (MiniCPM3 shape: 40 heads, latent
 ``roofline``: algorithmic bytes per decode layer (288 B per INT2 token, window
 rows, q and out) over the measured layer time, against 8 TB/s. ``traffic`` is
 taken from the committed rocprofv3 FETCH_SIZE/WRITE_SIZE summary when present.
-``cpu_baseline``: the oracle's dequantize-then-attention on the host cores for a
-bounded sample of config-2 sequences, scaled to one layer.
+``cpu_baseline``: the reference arithmetic restated in PyTorch (the oracle) on
+the host cores -- cfg0 codec + QDQ, a cfg1 layer of rotation + QDQ, a layer of
+dequantize-then-attention at cfg2 (``value``) and cfg4a -- median of 5 runs on
+bounded samples scaled to the full workload, with nproc and the CPU model.
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W]
 """
@@ -364,32 +366,88 @@ def extend_result(args, dev: str, layers: int = 2) -> dict:
 # ---------------------------------------------------------------------------
 # CPU baseline (oracle on the host cores)
 # ---------------------------------------------------------------------------
-def cpu_baseline(db: DecodeBench, seqs: int = 2):
-    from oracle import attention, layout, window
+def _cpu_model() -> str:
+    try:
+        for line in Path("/proc/cpuinfo").read_text().splitlines():
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
 
-    threads = os.cpu_count() or 1
-    torch.set_num_threads(threads)
-    c = db.caches[0]
-    D, R, P, W, L = db.D, db.R, db.P, db.W, db.L
-    pool = {
+
+def _median_runs(fn, runs: int = 5):
+    """1 warm-up, then ``runs`` timed calls; returns (median s, all s)."""
+    fn()
+    ts = []
+    for _ in range(runs):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return float(np.median(ts)), ts
+
+
+def _pool_np(c: dict) -> dict:
+    return {
         "codes": c["codes"].cpu().numpy(),
         "params": c["params"].cpu().numpy(),
         "rope": c["rope"].cpu().view(torch.int16).numpy().view(np.uint16),
         "hp": c["hp"].cpu().view(torch.int16).numpy().view(np.uint16),
     }
+
+
+def _attention_leg(db: "DecodeBench", seqs: int, batch: int):
+    """One layer of the oracle's dequantize-then-attention (torch CPU, FP32) over
+    ``seqs`` sequences of ``db``'s layer 0, scaled to ``batch`` sequences."""
+    from oracle import attention
+
+    c = db.caches[0]
+    pool = _pool_np(c)
     pt = db.kv_indices.cpu().numpy().reshape(db.B, -1)
     q = c["q"].cpu()
+    D = db.D
     slots = [(pt[b][:, None] * db.PAGE + np.arange(db.PAGE)).reshape(-1) for b in range(seqs)]
-    # warm-up on a short prefix, then time `seqs` full sequences
-    attention.decode(pool, q[:1, :, :D], q[:1, :, D:], slots[:1], [1024], [1], P, W, db.sm_scale, D, "fp32")
-    t0 = time.perf_counter()
-    attention.decode(pool, q[:seqs, :, :D], q[:seqs, :, D:], slots, [L] * seqs, list(range(1, seqs + 1)),
-                     P, W, db.sm_scale, D, "fp32")
-    dt = time.perf_counter() - t0
-    per_layer_us = dt / seqs * db.B * 1e6
-    return {"value": round(per_layer_us, 1), "unit": "us/layer", "cores": threads, "kind": "port",
-            "sample": f"oracle dequantize-then-attention (torch CPU, FP32) on {seqs} of the 32 sequences "
-                      f"x 16384 tokens of layer 0, scaled x{db.B // seqs} to one layer"}
+    lens = [int(v) for v in db.lengths[:seqs]]
+    med, ts = _median_runs(lambda: attention.decode(pool, q[:seqs, :, :D], q[:seqs, :, D:], slots, lens,
+                                                    list(range(1, seqs + 1)), db.P, db.W, db.sm_scale, D, "fp32"))
+    scale = batch / seqs
+    return {"value": round(med * scale * 1e6, 1), "unit": "us/layer", "median_s_sample": round(med, 4),
+            "runs_s": [round(t, 4) for t in ts], "sample": f"{seqs} of {batch} sequences, scaled x{scale:g}"}
+
+
+def cpu_baseline(db: "DecodeBench", dev: str):
+    """The reference arithmetic restated in PyTorch on the host cores (the
+    oracle): cfg0 codec + QDQ, one cfg1 layer of FP32 rotation GEMM + QDQ, and
+    one layer of dequantize-then-attention at cfg2 and cfg4a. Median of 5 runs
+    after one warm-up each, on bounded samples scaled to the full workload."""
+    from oracle import codec
+    from mla_kv_quant_amd import synth
+
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    legs = {}
+    # cfg0: codec + QDQ on [4096, 512] (rotated rows, oscar.py:120-144 / quantizer.py:102-124)
+    rot = synth.make_rotation(512, 90)
+    x0 = synth.make_latent(4096, 512, 8, seed=90)
+    med, ts = _median_runs(lambda: codec.rotate_quantize(x0, rot))
+    legs["cfg0_codec_qdq"] = {"value": round(med * 1e3, 2), "unit": "ms", "rows": 4096,
+                              "runs_s": [round(t, 4) for t in ts]}
+    # cfg1: one layer = FP32 rotation GEMM + QDQ of 131072 rows; sample 16384 rows, scaled x8
+    x1 = synth.make_latent(16384, 512, 5, seed=91)
+    med, ts = _median_runs(lambda: codec.rotate_quantize(x1, rot))
+    legs["cfg1_rotate_qdq_layer"] = {"value": round(med * 8 * 1e3, 1), "unit": "ms/layer",
+                                     "sample": "16384 of 131072 rows, scaled x8", "runs_s": [round(t, 4) for t in ts]}
+    # cfg2 / cfg4a: one layer of dequantize-then-attention
+    legs["cfg2_attention_layer"] = _attention_leg(db, 2, 32)
+    db4 = DecodeBench(1, dev, B=2, lengths=[16384] * 2, H=40, D=256, R=32, seed=4)
+    legs["cfg4a_attention_layer"] = _attention_leg(db4, 2, 64)
+    del db4
+    torch.cuda.empty_cache()
+    head = legs["cfg2_attention_layer"]
+    return {"value": head["value"], "unit": "us/layer", "cores": threads, "kind": "port",
+            "sample": "cfg2 leg: oracle dequantize-then-attention (torch CPU, FP32) on 2 of the 32 sequences x 16384 "
+                      "tokens of one layer, median of 5 runs, scaled x16 to one layer",
+            "nproc": threads, "cpu_model": _cpu_model(), "legs": legs}
 
 
 def read_traffic():
@@ -534,9 +592,20 @@ def main():
     db = DecodeBench(args.layers, dev)
     print(f"[bench] decode caches written for {args.layers} layers in {time.time() - t_setup:.1f}s", file=sys.stderr,
           flush=True)
-    ns_best = db.pick_splits([args.splits] if args.splits else [9, 17, 8, 16, 33])
+    # split policy: one working block per CU (num_kv_splits = ceil(CUs / B) INT2
+    # splits + the window split), fixed before timing; --splits overrides it.
+    # The reference's static 129 (serve.py:198) is timed beside it.
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    ns_best = args.splits if args.splits else -(-cus // db.B) + 1
+    db.alloc_scratch(129)
+    db.set_splits(129)
+    ms129 = time_loop(db.step, max(5, args.steps // 2), args.warmup)
+    db.alloc_scratch(ns_best)
+    db.set_splits(ns_best)
     ms = time_loop(db.step, args.steps, args.warmup)
     us_layer = ms * 1000.0 / args.layers
+    print(f"[bench] decode: {ns_best} splits {us_layer:.2f} us/layer, the reference's 129 splits "
+          f"{ms129 * 1000.0 / args.layers:.2f} us/layer", file=sys.stderr, flush=True)
     bpl = db.bytes_per_layer()
     # the dominant kernel (stage 1) timed alone: same events, same stream, one launch per layer
     ms1 = time_loop(db.step_partials, args.steps, args.warmup)
@@ -563,10 +632,11 @@ def main():
         "config": {"workload": "cfg2 decode: batch 32 x context 16384, 16 heads, latent 512, rope 64, "
                                "s4r16 window, page 64 shuffled, 27 layers with own buffers",
                    "batch": db.B, "context": db.L, "heads": db.H, "layers": args.layers,
-                   "num_kv_splits": ns_best},
+                   "num_kv_splits": ns_best, "split_policy": "ceil(CUs / B) + 1",
+                   "us_per_layer_at_129_splits": round(ms129 * 1000.0 / args.layers, 3)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": read_traffic(),
-                     "kernel": "decode_stage1<512,64,paged>", "us_per_launch": round(us_stage1, 3),
+                     "kernel": "decode_stage1<512,64,1>", "us_per_launch": round(us_stage1, 3),
                      "algorithmic_bytes_per_launch": b1,
                      "layer_frac": round(bpl / (us_layer * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
                      "copy_gbs": round(copy_gbs, 1),
@@ -586,7 +656,7 @@ def main():
     if not args.no_cpu:
         if not hasattr(db, "caches"):
             db = DecodeBench(1, dev)
-        result["cpu_baseline"] = cpu_baseline(db)
+        result["cpu_baseline"] = cpu_baseline(db, dev)
     print(json.dumps(result), flush=True)
 
 
