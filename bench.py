@@ -328,6 +328,8 @@ class ExtendBench:
                                  synth.make_normal((B * TQ, R), 64_000 + layer, device=dev)], 1).contiguous()
             self.layers.append(c)
         self.out = torch.empty(B * TQ, H, D, dtype=torch.bfloat16, device=dev)
+        # key rows gathered per call (one layer at a time: one workspace serves all layers)
+        self.ws = torch.empty(B * (PF + TQ), D + R, dtype=torch.bfloat16, device=dev)
         torch.cuda.synchronize()
 
     def step(self):
@@ -336,7 +338,7 @@ class ExtendBench:
         for c in self.layers:
             kernels.extend_fwd(c["q"], c["kc"], self.qo_indptr, self.kv_indptr, self.kv_indices, self.prefix,
                                self.req, c["codes"], c["params"], c["rope"], c["hp"], self.TQ, self.out,
-                               self.sm_scale, self.P, self.W, self.PAGE)
+                               self.sm_scale, self.P, self.W, self.PAGE, workspace=self.ws)
 
     def flops_per_layer(self) -> float:
         """Algorithmic flops: 2 H (2 D + R) per (query, visible key) pair."""

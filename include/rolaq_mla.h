@@ -217,14 +217,21 @@ int rolaq_decode_merge(const float* attn_logits, const float* attn_lse, const in
  * out: bf16 [T, H, D], strides (out_stride_t, out_stride_h), rotated frame.
  * max_q_len >= every chunk length (sizes the grid). (D, R) = (256, 32) or
  * (512, 64).
+ * workspace: caller-owned bf16 [workspace_rows, D + R], 16-byte aligned; the
+ * call first gathers every key row of the extended sequences into it
+ * (sequence b at rows koff_b .., koff_b = sum over b' < b of
+ * prefix_lens[b'] + chunk length b'), so workspace_rows must be at least
+ * sum_b (prefix_lens[b] + chunk length b). Rows past workspace_rows are never
+ * written (their keys then read as zeros: a short workspace gives wrong
+ * outputs, never an out-of-bounds access). Its contents are scratch.
  */
 int rolaq_extend_fwd(const void* q, int64_t q_stride_t, int64_t q_stride_h, const void* k_chunk,
                      int64_t kc_stride_t, const int32_t* qo_indptr, const int32_t* kv_indptr,
                      const int32_t* kv_indices, int page_size, const int64_t* prefix_lens,
                      const int64_t* req_idx, int max_reqs, const uint8_t* codes, const float* params,
                      const void* rope_buf, const void* hp_c, int B, int H, int D, int R, int P, int W,
-                     int max_q_len, float sm_scale, void* out, int64_t out_stride_t,
-                     int64_t out_stride_h, void* stream);
+                     int max_q_len, float sm_scale, void* workspace, int64_t workspace_rows, void* out,
+                     int64_t out_stride_t, int64_t out_stride_h, void* stream);
 
 /*
  * Cache rows as bf16 [latent | rope] rows (MHA-style prefill over a packed

@@ -44,7 +44,8 @@ SIGNATURES = {
                            c_int64, c_void_p],
     "rolaq_extend_fwd": [c_void_p, c_int64, c_int64, c_void_p, c_int64, c_void_p, c_void_p, c_void_p, c_int,
                          c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int,
-                         c_int, c_int, c_int, c_int, c_float, c_void_p, c_int64, c_int64, c_void_p],
+                         c_int, c_int, c_int, c_int, c_float, c_void_p, c_int64, c_void_p, c_int64, c_int64,
+                         c_void_p],
     "rolaq_assemble_rows": [c_void_p, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                             c_void_p, c_int, c_int, c_void_p, c_int64, c_void_p],
 }

@@ -64,7 +64,7 @@ extern "C" {
 
 const char* rolaq_last_error(void) { return g_err; }
 
-int rolaq_abi_version(void) { return 2; }
+int rolaq_abi_version(void) { return 3; }
 
 int rolaq_scatter_pack_rows(const float* x, int64_t x_stride, const int32_t* slots, int64_t n, int D,
                             int group_size, float threshold, double gain, uint8_t* codes, float* params,
@@ -370,15 +370,18 @@ int rolaq_extend_fwd(const void* q, int64_t q_stride_t, int64_t q_stride_h, cons
                      const int32_t* kv_indices, int page_size, const int64_t* prefix_lens,
                      const int64_t* req_idx, int max_reqs, const uint8_t* codes, const float* params,
                      const void* rope_buf, const void* hp_c, int B, int H, int D, int R, int P, int W, int max_q_len,
-                     float sm_scale, void* out, int64_t out_stride_t, int64_t out_stride_h, void* stream) {
+                     float sm_scale, void* workspace, int64_t workspace_rows, void* out, int64_t out_stride_t,
+                     int64_t out_stride_h, void* stream) {
   if (B < 0 || max_q_len < 0) return fail(ROLAQ_ERR_INVALID, "extend_fwd: B < 0 or max_q_len < 0");
   if (B == 0 || max_q_len == 0) { g_err[0] = '\0'; return ROLAQ_OK; }
   if (!((D == 256 && R == 32) || (D == 512 && R == 64)))
     return fail(ROLAQ_ERR_INVALID, "extend_fwd: (D, R) must be (256, 32) or (512, 64), got (%d, %d)", D, R);
   if (H <= 0 || H > 4096) return fail(ROLAQ_ERR_INVALID, "extend_fwd: head count %d out of range", H);
   if (!q || !k_chunk || !qo_indptr || !kv_indptr || !kv_indices || !prefix_lens || !req_idx || !codes || !params ||
-      !rope_buf || !hp_c || !out)
+      !rope_buf || !hp_c || !out || !workspace)
     return fail(ROLAQ_ERR_INVALID, "extend_fwd: null pointer");
+  if (workspace_rows < 1 || !aligned(workspace, 16))
+    return fail(ROLAQ_ERR_INVALID, "extend_fwd: workspace must be 16-byte aligned with at least one row");
   if (page_size < 1 || (page_size & (page_size - 1)))
     return fail(ROLAQ_ERR_INVALID, "extend_fwd: page_size must be a power of two, got %d", page_size);
   if (P < 0 || W < 0) return fail(ROLAQ_ERR_INVALID, "extend_fwd: negative window");
@@ -414,6 +417,8 @@ int rolaq_extend_fwd(const void* q, int64_t q_stride_t, int64_t q_stride_h, cons
   a.W = W;
   a.max_reqs = max_reqs;
   a.sm_scale = sm_scale;
+  a.ws = static_cast<uint16_t*>(workspace);
+  a.ws_rows = workspace_rows;
   a.out = static_cast<uint16_t*>(out);
   a.o_st = out_stride_t;
   a.o_sh = out_stride_h;

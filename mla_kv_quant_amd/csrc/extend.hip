@@ -9,11 +9,17 @@
 // W positions of the extended sequence, which are the BF16 window rows; the
 // chunk's rows enter as the given BF16 keys; attention is causal.
 //
-// Layout of the work: a block takes BM consecutive (token, head) query rows of
-// one sequence (all heads share the keys: MQA) and walks the keys in tiles of
-// 32. Each tile is built in LDS by 256 threads of the block -- key rows
-// [latent | rope] -- while the previous tile is being consumed,
-// double-buffered. Per wave and tile:
+// Layout of the work: two launches.
+//   gather  every key row of the extended sequences -- [latent | rope] bf16,
+//           INT2 rows dequantized and rounded once -- into the caller's
+//           workspace, sequence b at rows koff_b .. koff_b + prefix_b + q_b - 1
+//           (koff_b = sum over b' < b of prefix_b' + q_b'); HBM-bound, read
+//           once per call instead of once per query block.
+//   attend  a block takes BM consecutive (token, head) query rows of one
+//           sequence (all heads share the keys: MQA) and walks its keys in
+//           tiles of 32, each copied from the workspace into LDS by the whole
+//           block while the previous tile is consumed (double-buffered). Per
+//           wave and tile:
 //   S^T[32 keys, RW rows] = K . Q^T   on MFMA 16x16x32 (Q held in registers)
 //   softmax in the log2 domain against a fixed per-row reference (the row's
 //   maximum over the first tile); a block whose scores exceed it by more than
@@ -62,132 +68,56 @@ __device__ __forceinline__ float add_over_rows(float v) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
-// Where the rows of one key tile come from, per loader thread: key quad
-// kq (keys 4 kq .. 4 kq + 3 of the tile) and latent octets OPT * o .. .
-template <int D, int R>
-struct TileRaw {
-  static constexpr int OPT = ExtGeo<D, R>::OPT;
-  u32x4 lat[4][OPT];  // bf16 rows
-  uint32_t code[4];   // packed codes of the thread's octets (INT2 rows)
-  u32x4 rope[4];      // rope octet o (threads o < R / 8)
-  f32x2 prm[4];       // (scale, zero) of the INT2 rows' group
-  uint32_t mode;      // 2 bits per key: 0 zero, 1 bf16, 2 int2
-};
-
-// Pages of the prefix keys of a tile (page-table lookups), one tile ahead of
-// the data loads; the values are first used by the next tile's load_tile, so
-// no instruction of this tile waits on them (0 for keys without a page).
-template <int D, int R>
-__device__ __forceinline__ void lookup_tile(const ExtendArgs& a, int32_t pg[4], int k0, int kq, int64_t prefix,
-                                            int64_t kv0, int kend) {
-#pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    const int kp = k0 + 4 * kq + k;
-    pg[k] = (kp < kend && kp < prefix) ? gload<int32_t>(a.kv_indices + kv0 + (kp >> a.page_shift)) : 0;
-  }
+// Workspace row of key 0 of sequence b.
+__device__ __forceinline__ int64_t key_offset(const ExtendArgs& a, int b) {
+  int64_t off = 0;
+  for (int i = 0; i < b; ++i) off += a.prefix_lens[i] + (a.qo_indptr[i + 1] - a.qo_indptr[i]);
+  return off;
 }
 
-// INT2 = true: every key of the tile is an INT2 prefix row (the tile lies in
-// [P, min(prefix, L - W))), so no per-key source selection is needed.
-template <int D, int R, bool INT2>
-__device__ __forceinline__ void load_tile(const ExtendArgs& a, TileRaw<D, R>& t, const int32_t pg[4], int k0,
-                                          int kq, int o, int64_t qo0, int64_t prefix, int64_t L, int64_t req,
-                                          int kend) {
-  constexpr int NG = D / 128, OPT = ExtGeo<D, R>::OPT;
-  const int dlo = 8 * OPT * o;  // first latent column of this thread
-  const int g = dlo / 128;
-  if constexpr (INT2) {
-    const uint32_t coff = dlo / 4;  // elements dlo .. of the packed row start at byte dlo / 4
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const int kp = k0 + 4 * kq + k;
-      const uint32_t slot = ((uint32_t)pg[k] << a.page_shift) + (kp & ((1 << a.page_shift) - 1));
-      const uint64_t sl = slot;  // 64-bit offsets: a pool may exceed 4 GB per array
-      if constexpr (OPT == 2) t.code[k] = gload<uint32_t>(a.codes + sl * (D / 4) + coff);
-      else t.code[k] = gload<uint16_t>(a.codes + sl * (D / 4) + coff);
-      t.prm[k] = gload<f32x2>(a.params + sl * (2 * NG) + 2 * g);
-      t.rope[k] = o < R / 8 ? gload<u32x4>(a.rope + sl * R + 8 * o) : u32x4{0u, 0u, 0u, 0u};
-    }
-    t.mode = 0xAAu;
-    return;
-  }
-  // where each key's bytes are (all addresses first: the pages were loaded an
-  // iteration ago, and no load below may wait behind another)
-  const uint16_t* lat[4];
-  const uint16_t* rope[4];
-  const uint8_t* code[4];
-  const float* prm[4];
-  uint32_t mode = 0;
-#pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    const int kp = k0 + 4 * kq + k;
-    const int64_t slot = (int64_t)pg[k] * (1 << a.page_shift) + (kp & ((1 << a.page_shift) - 1));
-    lat[k] = nullptr;
-    rope[k] = nullptr;
-    code[k] = nullptr;
-    prm[k] = nullptr;
-    if (kp >= kend) continue;
-    if (kp >= prefix) {  // a row of the chunk itself: the given BF16 key
-      lat[k] = a.kc + (qo0 + kp - prefix) * a.kc_st + dlo;
-      rope[k] = a.kc + (qo0 + kp - prefix) * a.kc_st + D + 8 * o;
-      mode |= 1u << (2 * k);
-    } else if (kp < a.P || kp >= L - a.W) {  // BF16 window row
-      const int inner = kp < a.P ? kp : a.P + (kp - a.P) % (a.W > 0 ? a.W : 1);
-      lat[k] = a.hp + (1 + req * (a.P + a.W) + inner) * D + dlo;
-      rope[k] = a.rope + slot * R + 8 * o;
-      mode |= 1u << (2 * k);
-    } else {  // INT2 row
-      code[k] = a.codes + slot * (D / 4) + dlo / 4;
-      prm[k] = a.params + slot * 2 * NG + 2 * g;
-      rope[k] = a.rope + slot * R + 8 * o;
-      mode |= 2u << (2 * k);
-    }
-  }
-  t.mode = mode;
-  __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-  for (int k = 0; k < 4; ++k) {
-    const uint32_t m = (mode >> (2 * k)) & 3u;
-#pragma unroll
-    for (int j = 0; j < OPT; ++j) t.lat[k][j] = m == 1u ? gload<u32x4>(lat[k] + 8 * j) : u32x4{0u, 0u, 0u, 0u};
-    if constexpr (OPT == 2) t.code[k] = m == 2u ? gload<uint32_t>(code[k]) : 0u;
-    else t.code[k] = m == 2u ? uint32_t(gload<uint16_t>(code[k])) : 0u;
-    t.prm[k] = m == 2u ? gload<f32x2>(prm[k]) : f32x2{0.f, 0.f};
-    t.rope[k] = (m != 0u && o < R / 8) ? gload<u32x4>(rope[k]) : u32x4{0u, 0u, 0u, 0u};
-  }
-}
-
-// Dequantize (INT2 rows) and store one tile's key rows [key][latent | rope]
-// (bf16). The output MFMA reads the latent transposed out of the same rows.
-template <int D, int R, bool INT2>
-__device__ __forceinline__ void store_tile(const TileRaw<D, R>& t, uint8_t* buf, int kq, int o) {
-  using G = ExtGeo<D, R>;
-  constexpr int OPT = G::OPT;
-  uint8_t* kb = buf;
-#pragma unroll
-  for (int j = 0; j < OPT; ++j) {
-#pragma unroll
-    for (int k = 0; k < 4; ++k) {
-      const uint32_t m = (t.mode >> (2 * k)) & 3u;
-      u32x4 v;
-      if (INT2 || m == 2u) {
-        // (code - zero) * scale, rounded to bf16 as the reference's QDQ rows are
-        const uint32_t bits = OPT == 2 ? (t.code[k] >> (16 * j)) : t.code[k];
-        const float sc = t.prm[k].x, z = t.prm[k].y;
+// Key rows of sequence blockIdx.x (one thread per 16-byte chunk, rows strided
+// over blockIdx.y): chunk rows from k_chunk, prefix rows from the BF16 window
+// (t < P or t >= L - W of the extended length L) or the INT2 row
+// ((code - zero) * scale rounded to bf16), rope from rope_buf.
+template <int D, int R>
+__global__ __launch_bounds__(256) void extend_gather_kernel(ExtendArgs a) {
+  constexpr int DR = D + R, CPR = DR / 8, NG = D / 128;
+  const int b = blockIdx.x;
+  const int64_t qo0 = a.qo_indptr[b];
+  const int64_t Tq = a.qo_indptr[b + 1] - qo0;
+  const int64_t prefix = a.prefix_lens[b];
+  const int64_t L = prefix + Tq;
+  const int64_t req = a.req_idx[b];
+  const bool ring = req >= 0 && req < a.max_reqs;
+  const int P = ring ? a.P : 0, W = ring ? a.W : 0;
+  const int64_t koff = key_offset(a, b);
+  const int64_t kv0 = a.kv_indptr[b];
+  const int pmask = (1 << a.page_shift) - 1;
+  const int64_t n = min(L, a.ws_rows - koff) * CPR;
+  for (int64_t e = (int64_t)blockIdx.y * blockDim.x + threadIdx.x; e < n; e += (int64_t)gridDim.y * blockDim.x) {
+    const int64_t t = e / CPR;
+    const int c = (int)(e - t * CPR);
+    u32x4 v;
+    if (t >= prefix) {
+      v = gload<u32x4>(a.kc + (qo0 + t - prefix) * a.kc_st + 8 * c);
+    } else {
+      const int64_t slot = ((int64_t)a.kv_indices[kv0 + (t >> a.page_shift)] << a.page_shift) + (t & pmask);
+      if (c >= D / 8) {
+        v = gload<u32x4>(a.rope + slot * R + 8 * (c - D / 8));
+      } else if (t < P || t >= L - W) {
+        const int64_t inner = t < P ? t : P + (t - P) % (W > 0 ? W : 1);
+        v = gload<u32x4>(a.hp + (1 + req * (P + W) + inner) * D + 8 * c);
+      } else {
+        // elements 8c .. 8c + 7 sit in bytes 2c, 2c + 1 of the packed row
+        const uint32_t bits = gload<uint16_t>(a.codes + slot * (D / 4) + 2 * c);
+        const f32x2 sz = gload<f32x2>(a.params + slot * (2 * NG) + 2 * (c / 16));
         float f[8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) f[e] = (float((bits >> (2 * e)) & 3u) - z) * sc;
+        for (int k = 0; k < 8; ++k) f[k] = (float((bits >> (2 * k)) & 3u) - sz.y) * sz.x;
         v = u32x4{pack_bf16(f[0], f[1]), pack_bf16(f[2], f[3]), pack_bf16(f[4], f[5]), pack_bf16(f[6], f[7])};
-      } else {
-        v = t.lat[k][j];
       }
-      *reinterpret_cast<u32x4*>(kb + (4 * kq + k) * G::KSTR + 16 * (OPT * o + j)) = v;
     }
-  }
-  if (o < R / 8) {
-#pragma unroll
-    for (int k = 0; k < 4; ++k)
-      *reinterpret_cast<u32x4*>(kb + (4 * kq + k) * G::KSTR + 2 * D + 16 * o) = t.rope[k];
+    *reinterpret_cast<u32x4*>(a.ws + (koff + t) * DR + 8 * c) = v;
   }
 }
 
@@ -221,11 +151,7 @@ __global__ __launch_bounds__((64 * ExtGeo<D, R>::WAVES), 1) void extend_kernel(E
   if (r0 >= nrows) return;
   const int64_t prefix = a.prefix_lens[b];
   const int64_t L = prefix + Tq;
-  const int64_t req = a.req_idx[b];
-  // a request without ring rows (index outside [0, max_reqs)) has no BF16
-  // window: the writer stored none for it, so its prefix is read from the codes
-  if (req < 0 || req >= a.max_reqs) a.P = a.W = 0;
-  const int64_t kv0 = a.kv_indptr[b];
+  const int64_t koff = key_offset(a, b);
   // last query token of the block -> keys 0 .. prefix + t_last
   const int64_t t_last = min(nrows - 1, r0 + BM - 1) / a.H;
   const int kend = (int)(prefix + t_last + 1);
@@ -234,9 +160,28 @@ __global__ __launch_bounds__((64 * ExtGeo<D, R>::WAVES), 1) void extend_kernel(E
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int gq = lane >> 4, la = lane & 15;
-  // loader role: the first 256 threads build the tiles (key quad kq, octet o)
-  const int kq = (tid >> 5) & 7, o = tid & 31;
-  const bool ldr = tid < 256;
+  // tile copy: thread tid moves 16-byte chunks tid, tid + NT, ... of the tile's
+  // 32 key rows (keys past the block's last key, or past the workspace, are zeros)
+  constexpr int DR = D + R, CPR = DR / 8, CH = kExtKeys * CPR, NT = 64 * G::WAVES, NCH = (CH + NT - 1) / NT;
+  const int64_t krows = min((int64_t)kend, a.ws_rows - koff);
+  u32x4 raw[NCH];
+  auto load_keys = [&](int k0) {
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+      const int ci = tid + NT * j;
+      const int key = ci / CPR, c = ci - key * CPR;
+      const int64_t kp = k0 + key;
+      raw[j] = (ci < CH && kp < krows) ? gload<u32x4>(a.ws + (koff + kp) * DR + 8 * c) : u32x4{0u, 0u, 0u, 0u};
+    }
+  };
+  auto store_keys = [&](uint8_t* buf) {
+#pragma unroll
+    for (int j = 0; j < NCH; ++j) {
+      const int ci = tid + NT * j;
+      const int key = ci / CPR, c = ci - key * CPR;
+      if (ci < CH) *reinterpret_cast<u32x4*>(buf + key * G::KSTR + 16 * c) = raw[j];
+    }
+  };
 
   // ---- query rows of this wave: Q^T fragments and positions -----------------
   u32x4 qf[NBR][KSQ];
@@ -258,10 +203,6 @@ __global__ __launch_bounds__((64 * ExtGeo<D, R>::WAVES), 1) void extend_kernel(E
 #pragma unroll
   for (int nb = 0; nb < NBR; ++nb) qp[nb] = (int)qpos[nb];
 
-  // a tile of INT2 prefix rows only ([P, min(prefix, L - W))): loads without per-key selection
-  const int64_t int2_end = min(prefix, L - (int64_t)a.W);
-  auto int2_tile = [&](int t0) { return t0 >= a.P && (int64_t)t0 + kExtKeys <= int2_end; };
-
   f32x4 acc_o[NBR][ND];
   float m_ref[NBR], m_lane[NBR], l_run[NBR];
   bool redo = false;
@@ -274,26 +215,15 @@ __global__ __launch_bounds__((64 * ExtGeo<D, R>::WAVES), 1) void extend_kernel(E
       l_run[nb] = 0.f;
     }
 
-    TileRaw<D, R> raw;
-    int32_t sl[4];
-    if (ldr) {
-      lookup_tile<D, R>(a, sl, 0, kq, prefix, kv0, kend);
-      load_tile<D, R, false>(a, raw, sl, 0, kq, o, qo0, prefix, L, req, kend);
-      lookup_tile<D, R>(a, sl, kExtKeys, kq, prefix, kv0, kend);
-      store_tile<D, R, false>(raw, s_buf, kq, o);
-    }
+    load_keys(0);
+    store_keys(s_buf);
     __syncthreads();
 
     for (int it = 0; it < ntiles; ++it) {
       const uint8_t* kb = s_buf + (it & 1) * G::BUF;
       const int k0 = it * kExtKeys;
       // loads of the next tile first: they have this tile's compute to land
-      // (its pages were looked up an iteration ago)
-      if (ldr && it + 1 < ntiles) {
-        if (int2_tile(k0 + kExtKeys)) load_tile<D, R, true>(a, raw, sl, k0 + kExtKeys, kq, o, qo0, prefix, L, req, kend);
-        else load_tile<D, R, false>(a, raw, sl, k0 + kExtKeys, kq, o, qo0, prefix, L, req, kend);
-        lookup_tile<D, R>(a, sl, k0 + 2 * kExtKeys, kq, prefix, kv0, kend);
-      }
+      if (it + 1 < ntiles) load_keys(k0 + kExtKeys);
 
       // ---- scores S^T[key, row] --------------------------------------------
       f32x4 s[2][NBR];
@@ -370,10 +300,7 @@ __global__ __launch_bounds__((64 * ExtGeo<D, R>::WAVES), 1) void extend_kernel(E
       }
 
       // ---- next tile into the other buffer (last read before the previous barrier)
-      if (ldr && it + 1 < ntiles) {
-        if (int2_tile(k0 + kExtKeys)) store_tile<D, R, true>(raw, s_buf + ((it + 1) & 1) * G::BUF, kq, o);
-        else store_tile<D, R, false>(raw, s_buf + ((it + 1) & 1) * G::BUF, kq, o);
-      }
+      if (it + 1 < ntiles) store_keys(s_buf + ((it + 1) & 1) * G::BUF);
       __syncthreads();
     }
 
@@ -421,6 +348,7 @@ hipError_t rolaq_launch_extend(const rolaq::ExtendArgs& a, int D, int R, int max
     const hipError_t e = hipFuncSetAttribute((const void*)extend_kernel<DD, RR>,                        \
                                              hipFuncAttributeMaxDynamicSharedMemorySize, lds);          \
     if (e != hipSuccess) return e;                                                                      \
+    hipLaunchKernelGGL((extend_gather_kernel<DD, RR>), dim3((unsigned)a.B, 64), dim3(256), 0, stream, a); \
     hipLaunchKernelGGL((extend_kernel<DD, RR>), grid, dim3(64 * G::WAVES), lds, stream, a);             \
     return hipGetLastError();                                                                           \
   }

@@ -87,6 +87,8 @@ struct ExtendArgs {
   int B, H, P, W;
   int max_reqs;             // req_idx outside [0, max_reqs) reads no window rows
   float sm_scale;
+  uint16_t* ws;             // workspace: key rows [ws_rows, D + R] bf16 (gathered per call)
+  int64_t ws_rows;
   uint16_t* out;            // [T, H, D] bf16, strides (o_st, o_sh)
   int64_t o_st, o_sh;
 };

@@ -294,10 +294,13 @@ def extend_fwd(q: torch.Tensor, k_chunk: torch.Tensor, qo_indptr: torch.Tensor, 
                kv_indices: torch.Tensor, prefix_lens: torch.Tensor, req_idx: torch.Tensor, codes: torch.Tensor,
                params: torch.Tensor, rope_buf: torch.Tensor, hp_c: torch.Tensor, max_q_len: int,
                out: torch.Tensor, sm_scale: float, P: int, W: int, page_size: int = 1,
-               max_reqs: int | None = None) -> torch.Tensor:
+               max_reqs: int | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
     """Causal extend over the packed prefix + the chunk: ``q [T, H, D+R]`` -> ``out [T, H, D]``.
 
-    ``max_reqs`` as for :func:`decode_fwd`."""
+    ``max_reqs`` as for :func:`decode_fwd`. ``workspace``: bf16
+    ``[rows, D + R]`` with ``rows >= sum(prefix_lens) + T`` (the key rows of
+    the extended sequences are gathered into it); allocated here when not
+    given, which reads ``prefix_lens`` back to the host."""
     dev = q.device
     _need(q, "q", torch.bfloat16, dev, 3)
     T, H, DR = q.shape
@@ -328,11 +331,18 @@ def extend_fwd(q: torch.Tensor, k_chunk: torch.Tensor, qo_indptr: torch.Tensor, 
     if out.shape[0] < T or tuple(out.shape[1:]) != (H, D) or out.stride(2) != 1:
         raise ValueError("out must be [T, H, D] with a contiguous last dim")
     mr = _ring_reqs(hp_c, P, W, max_reqs)
+    if workspace is None:
+        rows = int(prefix_lens[:B].sum().item()) + int(qo_indptr[B].item()) - int(qo_indptr[0].item())
+        workspace = torch.empty(max(rows, 1), DR, dtype=torch.bfloat16, device=dev)
+    _need(workspace, "workspace", torch.bfloat16, dev, 2)
+    _contig(workspace, "workspace")
+    if workspace.shape[1] != DR:
+        raise ValueError("workspace must be [rows, D + R]")
     _lib.check(_lib.load().rolaq_extend_fwd(
         _p(q), q.stride(0), q.stride(1), _p(k_chunk), k_chunk.stride(0), _p(qo_indptr), _p(kv_indptr),
         _p(kv_indices), int(page_size), _p(prefix_lens), _p(req_idx), mr, _p(codes), _p(params), _p(rope_buf),
-        _p(hp_c), B, H, D, R, int(P), int(W), int(max_q_len), float(sm_scale), _p(out), out.stride(0),
-        out.stride(1), _stream(q)))
+        _p(hp_c), B, H, D, R, int(P), int(W), int(max_q_len), float(sm_scale), _p(workspace),
+        workspace.shape[0], _p(out), out.stride(0), out.stride(1), _stream(q)))
     return out
 
 

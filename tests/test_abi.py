@@ -30,7 +30,7 @@ def test_library_exports_every_declared_symbol():
         assert hasattr(lib, name), name
     # every declared symbol has a ctypes signature in the binding
     assert set(declared_symbols()) - {"rolaq_last_error"} <= set(_lib.SIGNATURES)
-    assert lib.rolaq_abi_version() == 2
+    assert lib.rolaq_abi_version() == 3
 
 
 def test_invalid_arguments_are_rejected_before_any_launch():
@@ -93,8 +93,8 @@ def test_invalid_arguments_are_rejected_before_any_launch():
     bad[15] = 384
     assert lib.rolaq_norm_write_rows(*bad) == _lib.ROLAQ_ERR_INVALID and b"(D, R)" in lib.rolaq_last_error()
     # extend: shape and pointer checks, empty batch is a no-op
-    eargs = [p, 40 * 288, 288, p, 288, p, p, p, 16, p, p, 4, p, p, p, p, 4, 40, 256, 32, 4, 16, 2048, 0.1, p,
-             40 * 256, 256, None]
+    eargs = [p, 40 * 288, 288, p, 288, p, p, p, 16, p, p, 4, p, p, p, p, 4, 40, 256, 32, 4, 16, 2048, 0.1, p, 1,
+             p, 40 * 256, 256, None]
     bad = list(eargs)
     bad[18], bad[19] = 384, 32
     assert lib.rolaq_extend_fwd(*bad) == _lib.ROLAQ_ERR_INVALID and b"(D, R)" in lib.rolaq_last_error()
@@ -107,6 +107,12 @@ def test_invalid_arguments_are_rejected_before_any_launch():
     bad = list(eargs)
     bad[11] = -2
     assert lib.rolaq_extend_fwd(*bad) == _lib.ROLAQ_ERR_INVALID and b"max_reqs" in lib.rolaq_last_error()
+    bad = list(eargs)
+    bad[24] = None
+    assert lib.rolaq_extend_fwd(*bad) == _lib.ROLAQ_ERR_INVALID and b"null" in lib.rolaq_last_error()
+    bad = list(eargs)
+    bad[25] = 0
+    assert lib.rolaq_extend_fwd(*bad) == _lib.ROLAQ_ERR_INVALID and b"workspace" in lib.rolaq_last_error()
     bad = list(eargs)
     bad[16] = 0
     assert lib.rolaq_extend_fwd(*bad) == _lib.ROLAQ_OK
