@@ -65,10 +65,11 @@ __global__ __launch_bounds__(256) void pack_rows_kernel(const T* __restrict__ x,
 #pragma unroll
   for (int o = 1; o < 16; o <<= 1) q += __shfl_xor(q, o);
   const float std_ = sqrtf(q * (1.0f / 128.0f) + 1e-08f);
+  const float rstd = 1.0f / std_;
   uint32_t bits = 0;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    const float nrm = v[i] / std_;  // correctly rounded, as oscar.py:135 divides
+    const float nrm = div_by(v[i], std_, rstd);  // correctly rounded, as oscar.py:135 divides
     const uint32_t c = uint32_t(nrm >= -thr) + uint32_t(nrm >= 0.f) + uint32_t(nrm >= thr);
     bits |= c << (2 * i);
   }

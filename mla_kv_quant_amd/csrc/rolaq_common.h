@@ -58,6 +58,16 @@ __device__ __forceinline__ uint16_t float_to_bf16(float f) {
   return uint16_t(pack_bf16(f, 0.0f) & 0xffffu);
 }
 
+// The correctly rounded FP32 quotient d / s from y = RN(1 / s) (one true
+// division per divisor): q0 = RN(d y), the exact remainder r = d - q0 s, then
+// RN(q0 + r y) (Markstein's quotient correction with a fused multiply-add,
+// P. Markstein, IBM J. Res. Dev. 34(1), 1990). Used where many values share a
+// divisor; checked against true division in tests/test_division_identity.py.
+__device__ __forceinline__ float div_by(float d, float s, float y) {
+  const float q0 = d * y;
+  return fmaf(fmaf(-q0, s, d), y, q0);
+}
+
 // Load through a global (address space 1) pointer: a global_load, which only
 // vmcnt tracks. A load through a generic pointer becomes flat_load, which LDS
 // waits (lgkmcnt) must also drain.

@@ -313,15 +313,16 @@ __global__ __launch_bounds__(64 * kWriterWaves, 1) void writer_kernel(WriterArgs
         }
       q = sum_over_rows(q);
       const float std_ = sqrtf(q * (1.0f / 128.0f) + 1e-08f);
-      // code = #{-t, 0, t <= normalized}, normalized = (x - mean) / std with a
-      // correctly rounded FP32 division (oscar.py:135-140, operation for operation)
+      // code = #{-t, 0, t <= normalized}, normalized = (x - mean) / std, the
+      // correctly rounded FP32 quotient (oscar.py:135-140, operation for operation)
       const float t = a.thr;
+      const float rstd = 1.0f / std_;
       uint32_t word[2] = {0u, 0u};
 #pragma unroll
       for (int mb = 0; mb < 8; ++mb)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float nrm = acc[mb][nb][i] / std_;
+          const float nrm = div_by(acc[mb][nb][i], std_, rstd);
           const uint32_t c = uint32_t(nrm >= -t) + uint32_t(nrm >= 0.f) + uint32_t(nrm >= t);
           word[mb >> 2] |= c << (2 * (4 * (mb & 3) + i));
         }
