@@ -184,8 +184,8 @@ __global__ __launch_bounds__(64 * kWriterWaves, 1) void writer_kernel(WriterArgs
 #pragma unroll
       for (int nb = 0; nb < 4; ++nb) xb[d][nb] = xload(rs, nb, d);
   }
-  // low dwords of the int64 row metadata (sequence lengths, positions and
-  // request indices fit in 32 bits; -1 stays -1)
+  // low dwords of the int64 row metadata (sequence lengths and positions are
+  // below 2^31 tokens; request indices are checked to fit, -1 stays -1)
   const int32_t* seq32 = reinterpret_cast<const int32_t*>(a.seq_lens);
   // decode rows (no positions) sit at seq_len - 1: read seq_lens there instead
   const int32_t* pos32 = reinterpret_cast<const int32_t*>(a.positions ? a.positions : a.seq_lens);
@@ -270,7 +270,10 @@ __global__ __launch_bounds__(64 * kWriterWaves, 1) void writer_kernel(WriterArgs
       slot[nb] = a.loc[r];
       seq[nb] = seq32[2 * r];
       pos[nb] = pos32[2 * r] + pos_adj;
-      req[nb] = req32[2 * r];
+      // a request index that does not fit 32 bits is outside [0, max_reqs):
+      // no ring row (its high dword is not the sign extension of the low one)
+      const int32_t rlo = req32[2 * r], rhi = req32[2 * r + 1];
+      req[nb] = rhi == (rlo >> 31) ? rlo : -1;
     }
 #pragma unroll
     for (int nb = 0; nb < 4; ++nb) {

@@ -186,3 +186,38 @@ def test_fused_writer_unrotated_layer_and_fallbacks():
     assert writer.try_fast_decode_store(pool, 0, torch.from_numpy(loc).to(DEV), x.to(DEV), pe.to(DEV))
     torch.cuda.synchronize()
     _compare_layer(pool, 0, ref, loc, 1e-5)
+
+
+def test_writer_request_index_beyond_32_bits_has_no_ring_rows():
+    """req_idx is int64: an index whose low 32 bits name a valid request but
+    which does not fit 32 bits is outside [0, max_reqs) (mla_fused_writer.py:41)
+    and claims no ring row; the codes are written as for any row."""
+    from mla_kv_quant_amd import kernels
+
+    D, R, P, W, max_reqs, n = 512, 64, 4, 16, 4, 40
+    rot = synth.make_rotation(D, 3).to(torch.bfloat16).t().contiguous().to(DEV)
+    x = synth.make_latent(n, D, 5, seed=4, device=DEV)
+    pe = synth.make_normal((n, R), 5, device=DEV)
+    loc = torch.arange(1, n + 1, device=DEV)
+    pos = torch.arange(n, device=DEV)
+    seq = torch.full((n,), n, device=DEV)
+    outs = []
+    for rq in (-1, (1 << 32) + 1):
+        bufs = {
+            "codes": torch.zeros(n + 1, D // 4, dtype=torch.uint8, device=DEV),
+            "params": torch.zeros(n + 1, D // 128, 2, device=DEV),
+            "rope": torch.zeros(n + 1, R, dtype=torch.bfloat16, device=DEV),
+            "hp": torch.zeros(1 + max_reqs * (P + W), D, dtype=torch.bfloat16, device=DEV),
+            "row": torch.full((n + 1,), -7, dtype=torch.int32, device=DEV),
+            "owner": torch.zeros(1 + max_reqs * (P + W), dtype=torch.int32, device=DEV),
+        }
+        kernels.write_rows(x, pe, rot, loc, seq, pos, torch.full((n,), rq, dtype=torch.int64, device=DEV),
+                           bufs["codes"], bufs["params"], bufs["rope"], bufs["hp"], bufs["row"], bufs["owner"],
+                           P, W, max_reqs, 0.9810652732849121, 1.16)
+        torch.cuda.synchronize()
+        outs.append(bufs)
+    a, b = outs
+    assert not b["hp"].view(torch.int16).any() and not b["owner"].any()
+    assert (b["row"][1:] == -1).all()
+    for k in ("codes", "params", "rope", "row"):
+        assert torch.equal(a[k], b[k]), k
