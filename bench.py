@@ -61,6 +61,8 @@ def parse():
     ap.add_argument("--no-extend", action="store_true")
     ap.add_argument("--no-reported", action="store_true", help="skip the cfg3 / cfg4a decode lines")
     ap.add_argument("--reported-only", action="store_true", help="only the cfg3 / cfg4a decode lines")
+    ap.add_argument("--read-probe", action="store_true",
+                    help="only time a sum over 4 GiB (the achievable read-only HBM rate)")
     ap.add_argument("--copy-probe", action="store_true",
                     help="only time a 1 GiB device copy (the reference kernel for rocprofv3 byte counters)")
     return ap.parse_args()
@@ -463,6 +465,20 @@ def read_traffic():
     return None
 
 
+def read_probe(nbytes: int = 4 << 30, reps: int = 10) -> float:
+    """Achievable HBM read rate: GB/s over ``nbytes`` read once and reduced to
+    a few bytes (a read-only stream like decode's), the better of torch's sum
+    over fp32 and a bf16 matrix-vector product (rocBLAS GEMV)."""
+    x = torch.empty(nbytes // 4, dtype=torch.float32, device="cuda").fill_(1.0)
+    ms_sum = time_loop(lambda: x.sum(), reps, 2)
+    a = x.view(torch.bfloat16).view(-1, 8192)
+    v = torch.ones(8192, dtype=torch.bfloat16, device="cuda")
+    ms_mv = time_loop(lambda: torch.mv(a, v), reps, 2)
+    del x, a
+    torch.cuda.empty_cache()
+    return nbytes / (min(ms_sum, ms_mv) * 1e-3) / 1e9
+
+
 def copy_probe(nbytes: int = 1 << 30, reps: int = 10) -> float:
     """Achievable HBM rate: GB/s (read + write) of a device-to-device copy of ``nbytes``."""
     src = torch.empty(nbytes // 4, dtype=torch.float32, device="cuda").fill_(1.0)
@@ -576,6 +592,9 @@ def main():
     if args.copy_probe:
         print(json.dumps({"copy_gbs": round(copy_probe(), 1), "bytes": 1 << 30}), flush=True)
         return
+    if args.read_probe:
+        print(json.dumps({"read_gbs": round(read_probe(), 1), "bytes": 4 << 30}), flush=True)
+        return
     from mla_kv_quant_amd import _lib
 
     _lib.load()
@@ -615,6 +634,7 @@ def main():
     b1 = db.bytes_per_layer(with_out=False)
     achieved = b1 / (us_stage1 * 1e-6) / 1e9
     copy_gbs = copy_probe()
+    read_gbs = read_probe()
     print(f"[bench] decode: {us_layer:.2f} us/layer; stage 1 {us_stage1:.2f} us/launch, {achieved:.0f} GB/s "
           f"(device copy {copy_gbs:.0f} GB/s)", file=sys.stderr, flush=True)
 
@@ -642,6 +662,8 @@ def main():
                      "algorithmic_bytes_per_launch": b1,
                      "layer_frac": round(bpl / (us_layer * 1e-6) / 1e9 / HBM_PEAK_GBS, 4),
                      "copy_gbs": round(copy_gbs, 1),
+                     "read_gbs": round(read_gbs, 1),
+                     "frac_of_read": round(achieved / read_gbs, 4),
                      "frac_of_copy": round(achieved / copy_gbs, 4),
                      "mfma_frac": round(db.flops_per_layer() / (us_stage1 * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4)},
     }
