@@ -191,7 +191,25 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
   const int b = nhb > 1 ? (lin / nhb) / (int)gridDim.y : (int)blockIdx.x;
   const int h0 = 16 * HG * hb;
   const int nh = min(16 * HG, a.H - h0);  // heads of this block
+  const int tid = threadIdx.x, lane = tid & 63, la = lane & 15, gq = lane >> 4;
+  const int gl = lane_group<D>(gq), s0 = lane_word0<D>(gq);
+
+  // The query loads and the sequence's metadata loads go out together, first
+  // (the tile pipeline waits on both, and on the page lookups that follow).
+  u32x4 qB[HG][KL], qR[HG][KR];
+#pragma unroll
+  for (int hg = 0; hg < HG; ++hg) {
+    const uint16_t* qh = a.q + b * a.q_sb + (int64_t)min(h0 + 16 * hg + la, a.H - 1) * a.q_sh;
+#pragma unroll
+    for (int j = 0; j < KL; ++j) qB[hg][j] = gload<u32x4>(qh + 128 * gl + 16 * (s0 + j / 2) + 8 * (j & 1));
+#pragma unroll
+    for (int kr = 0; kr < KR; ++kr) qR[hg][kr] = gload<u32x4>(qh + D + 32 * kr + 8 * gq);
+  }
   const int ns = a.num_kv_splits[b];
+  const int kv0 = a.kv_indptr[b], kv1 = a.kv_indptr[b + 1];
+  const int64_t req = a.req_idx[b];
+  const int64_t slv = (a.seq_lens ? a.seq_lens : a.req_idx)[b];  // no branch before the loads
+  const int L = a.seq_lens ? (int)slv : kv1 - kv0;
   const int nq = min(max(ns - 1, 1), a.S1 - 1);
   if (split > nq) return;
   if (split == nq) {
@@ -199,9 +217,6 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
     return;
   }
 
-  const int kv0 = a.kv_indptr[b];
-  const int L = a.seq_lens ? (int)a.seq_lens[b] : a.kv_indptr[b + 1] - kv0;
-  const int64_t req = a.req_idx[b];
   // a request without ring rows (index outside [0, max_reqs)) has no window:
   // the writer stored none for it, so every position is read from its codes
   const bool has_ring = req >= 0 && req < a.max_reqs;
@@ -213,11 +228,14 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
   const int ntiles = hi > lo ? (hi + kTile - 1) / kTile - t_first : 0;
   const int has_win = nw > 0 ? 1 : 0;
   const int U = ntiles + has_win;
-  // ceil(U s / nq): unit 0 (the window) always goes to split 0
-  const int ub = (int)(((int64_t)U * split + nq - 1) / nq), ue = (int)(((int64_t)U * (split + 1) + nq - 1) / nq);
+  // ceil(U s / nq): unit 0 (the window) always goes to split 0 (32-bit
+  // division whenever U (s + 1) + nq fits, as it does below 2^27 tokens)
+  const uint64_t num_b = (uint64_t)U * split + nq - 1, num_e = (uint64_t)U * (split + 1) + nq - 1;
+  const bool narrow = num_e < (1ull << 32);
+  const int ub = narrow ? (int)((uint32_t)num_b / (uint32_t)nq) : (int)(num_b / nq);
+  const int ue = narrow ? (int)((uint32_t)num_e / (uint32_t)nq) : (int)(num_e / nq);
   const bool win_block = has_win && ub == 0 && ue > 0;  // this block holds unit 0
 
-  const int tid = threadIdx.x, lane = tid & 63, la = lane & 15, gq = lane >> 4;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const bool win_mine = win_block && wave == 0;
   // INT2 units of this wave: u0, u0 + 4, ... below ue
@@ -226,29 +244,9 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
   const int n = u0 < ue ? (ue - u0 + kWaves - 1) / kWaves : 0;
   const int T0 = t_first + u0 - has_win;  // tile of INT2 unit i: T0 + 4i
 
-  const int gl = lane_group<D>(gq), s0 = lane_word0<D>(gq);
   const int pmask = (1 << a.page_shift) - 1;
   uint8_t* const wbuf = s_buf + wave * G::WBUF;
   const float sl2 = a.sm_scale * kLog2e;
-
-  // ---- query operands (registers) ---------------------------------------------
-  u32x4 qB[HG][KL], qR[HG][KR];
-#pragma unroll
-  for (int hg = 0; hg < HG; ++hg) {
-    const int h = h0 + 16 * hg + la;
-    const bool hv = h < a.H;
-    const uint16_t* qh = a.q + b * a.q_sb + (int64_t)min(h, a.H - 1) * a.q_sh;
-#pragma unroll
-    for (int j = 0; j < KL; ++j) {
-      const u32x4 v = gload<u32x4>(qh + 128 * gl + 16 * (s0 + j / 2) + 8 * (j & 1));
-      qB[hg][j] = hv ? pi_permute(v) : u32x4{0u, 0u, 0u, 0u};
-    }
-#pragma unroll
-    for (int kr = 0; kr < KR; ++kr) {
-      const u32x4 v = gload<u32x4>(qh + D + 32 * kr + 8 * gq);
-      qR[hg][kr] = hv ? v : u32x4{0u, 0u, 0u, 0u};
-    }
-  }
 
   // ---- per-wave softmax state and accumulators ----------------------------------
   f32x4 O[HG][NB];
@@ -276,6 +274,45 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
     }
   };
 
+  // ---- prologue: the first tile's pages (the query is in flight already), ------
+  // the buffer and state set-up while they travel, then the first tile's loads
+  TileRegs<D, R> dc, dn;  // the two tile register slots
+  int32_t pgc[2], pgn[2];  // their pages
+  const int nl = n - 1;
+  if (n > 0) {
+    lookup(0, pgc);
+    lookup(min(1, nl), pgn);
+  }
+  __builtin_amdgcn_sched_barrier(0);
+
+  // while they are in flight: this wave's buffer starts as zeros (see the
+  // pending-output rule below), and the first pass's state
+  u32x4 Ph[HG], Pl[HG];
+  auto init_pass = [&]() {
+#pragma unroll
+    for (int hg = 0; hg < HG; ++hg) {
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) O[hg][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+      m_seen[hg] = kNoRef;
+      l_lane[hg] = 0.f;
+      Ph[hg] = Pl[hg] = u32x4{0u, 0u, 0u, 0u};
+    }
+  };
+#pragma unroll
+  for (int k = 0; k < G::WBUF / 1024; ++k) lds_store128(wbuf + 1024 * k + 16 * lane, u32x4{0u, 0u, 0u, 0u});
+  init_pass();
+  __builtin_amdgcn_sched_barrier(0);
+  if (n > 0) load(0, pgc, dn);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+  for (int hg = 0; hg < HG; ++hg) {
+    const bool hv = h0 + 16 * hg + la < a.H;
+#pragma unroll
+    for (int j = 0; j < KL; ++j) qB[hg][j] = hv ? pi_permute(qB[hg][j]) : u32x4{0u, 0u, 0u, 0u};
+#pragma unroll
+    for (int kr = 0; kr < KR; ++kr) qR[hg][kr] = hv ? qR[hg][kr] : u32x4{0u, 0u, 0u, 0u};
+  }
+
   // The output contraction of a tile runs during the next tile's expansion:
   // word step s of tile i + 1 first reads tile i's V^T for N-blocks 4s..4s+3
   // (LDS elements 64s..64s+63), then writes its own expanded chunks to those
@@ -285,7 +322,6 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
   // the start of a pass they are zero and the buffer holds finite values
   // (zeros, or rows of the previous pass), so the first step's contraction
   // adds exactly 0.
-  u32x4 Ph[HG], Pl[HG];
 
   // softmax of one tile (scores S, validity of token 16 mb + 4 gq + r) into Ph / Pl
   auto softmax = [&](f32x4 (&S)[2][HG], auto valid, bool first) {
@@ -443,122 +479,104 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
 #pragma unroll
       for (int mb = 0; mb < 2; ++mb) S[mb][0] += S2[mb][0];
     }
-    softmax(S, [&](int tok) { return base + tok >= lo && base + tok < hi; }, first);
+    if (base >= lo && base + kTile <= hi)  // an interior tile: every token is an INT2 one
+      softmax(S, [](int) { return true; }, first);
+    else
+      softmax(S, [&](int tok) { return base + tok >= lo && base + tok < hi; }, first);
   };
 
-  // window tile: rows 0 .. nw-1 are positions [0, n_sink) U [rec_lo, L) read
-  // from the ring rows of hp_c (BF16), staged into wave 0's buffer by the
-  // whole block in the expanded layout, then scored from LDS by wave 0 (always
-  // the first tile of wave 0's pass: no output is pending)
+  // window tile: rows 0 .. nw-1 are positions [0, n_sink) U [rec_lo, L), the
+  // ring rows of hp_c (BF16). Wave 0 alone loads them in the score operand's
+  // layout, scores them and stores them into its buffer in the expanded
+  // layout, where the next tile's steps contract them like an INT2 tile (it is
+  // always the first unit of wave 0's pass: no output is pending before it).
   auto win_pos = [&](int i) { return i < n_sink ? i : rec_lo + (i - n_sink); };
-  auto stage_window = [&]() {
-    constexpr int CPR = D / 8;  // 16-byte chunks of a row in feature order
-    for (int k = tid; k < kTile * CPR; k += kThreads) {
-      const int i = k / CPR, c = k % CPR;
-      u32x4 v = {0u, 0u, 0u, 0u};
-      if (i < nw) {
-        const int pos = win_pos(i);
-        const int inner = pos < P ? pos : P + (pos - P) % max(W, 1);
-        const int64_t ring = 1 + req * (P + W) + inner;
-        v = pi_permute(gload<u32x4>(a.hp + ring * D + 8 * c));
-      }
-      // features 8c .. 8c+7: group g, word s, half hf -> lane group and K-step
-      const int g = c / 16, s = (c % 16) / 2, hf = c & 1;
-      const int gqc = D == 512 ? g : 2 * g + s / 4;
-      const int j = 2 * (s - lane_word0<D>(gqc)) + hf;
-      lds_store128(s_buf + i * ROWB + 16 * ((4 * j + gqc) ^ sw(i)), v);
+  auto window_tile = [&](bool first) {
+    f32x4 S[2][HG];
+    u32x4 c[2][KL], rp[2][KR];  // both M-blocks' loads in flight together
+    int32_t pg[2];
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb) pg[mb] = page_of(win_pos(min(16 * mb + la, nw - 1)));
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb) {
+      const int pos = win_pos(min(16 * mb + la, nw - 1));
+      const int inner = pos < P ? pos : P + (pos - P) % max(W, 1);
+      const uint16_t* row = a.hp + (1 + req * (P + W) + inner) * D + 128 * gl + 16 * s0;
+#pragma unroll
+      for (int j = 0; j < KL; ++j) c[mb][j] = gload<u32x4>(row + 16 * (j / 2) + 8 * (j & 1));
+      const int64_t slot = ((int64_t)pg[mb] << a.page_shift) + (pos & pmask);
+#pragma unroll
+      for (int kr = 0; kr < KR; ++kr) rp[mb][kr] = gload<u32x4>(a.rope + slot * R + 32 * kr + 8 * gq);
     }
-  };
-  auto window_rope = [&](u32x4 (&rp)[2][KR]) {
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb) {
       const int i = 16 * mb + la;
-      const int pos = win_pos(min(i, nw - 1));
-      const int64_t slot = ((int64_t)page_of(pos) << a.page_shift) + (pos & pmask);
-#pragma unroll
-      for (int kr = 0; kr < KR; ++kr) {
-        const u32x4 v = gload<u32x4>(a.rope + slot * R + 32 * kr + 8 * gq);
-        rp[mb][kr] = i < nw ? v : u32x4{0u, 0u, 0u, 0u};
-      }
-    }
-  };
-  auto window_tile = [&](const u32x4 (&rp)[2][KR], bool first) {
-    f32x4 S[2][HG];
-#pragma unroll
-    for (int mb = 0; mb < 2; ++mb) {
 #pragma unroll
       for (int hg = 0; hg < HG; ++hg) S[mb][hg] = f32x4{0.f, 0.f, 0.f, 0.f};
-      const int row = 16 * mb + la;
-      const uint8_t* rowp = wbuf + row * ROWB;
 #pragma unroll
-      for (int j = 0; j < KL; ++j) {
-        const u32x4 c = lds_load128(rowp + 16 * ((4 * j + gq) ^ sw(row)));
+      for (int kr = 0; kr < KR; ++kr) {
+        const u32x4 v = i < nw ? rp[mb][kr] : u32x4{0u, 0u, 0u, 0u};
 #pragma unroll
-        for (int hg = 0; hg < HG; ++hg) S[mb][hg] = mfma16x16x32(c, qB[hg][j], S[mb][hg]);
+        for (int hg = 0; hg < HG; ++hg) S[mb][hg] = mfma16x16x32(v, qR[hg][kr], S[mb][hg]);
       }
 #pragma unroll
-      for (int kr = 0; kr < KR; ++kr)
+      for (int j = 0; j < KL; ++j) {
+        const u32x4 v = i < nw ? pi_permute(c[mb][j]) : u32x4{0u, 0u, 0u, 0u};
+        lds_store128(wb[mb][j & 1] + 128 * (j >> 1), v);  // K-step j of row 16 mb + la
 #pragma unroll
-        for (int hg = 0; hg < HG; ++hg) S[mb][hg] = mfma16x16x32(rp[mb][kr], qR[hg][kr], S[mb][hg]);
+        for (int hg = 0; hg < HG; ++hg) S[mb][hg] = mfma16x16x32(v, qB[hg][j], S[mb][hg]);
+      }
     }
     softmax(S, [&](int tok) { return tok < nw; }, first);
   };
 
-  // this wave's buffer starts as zeros (see the pending-output rule above)
-#pragma unroll
-  for (int k = 0; k < G::WBUF / 1024; ++k) lds_store128(wbuf + 1024 * k + 16 * lane, u32x4{0u, 0u, 0u, 0u});
-
   // ---- passes (the second only when a score outran the reference) ---------------
-  TileRegs<D, R> dc, dn;  // tile being computed / tile in flight
-  int32_t pgc[2], pgn[2];  // their pages
   for (int pass = 0; pass < 2; ++pass) {
-#pragma unroll
-    for (int hg = 0; hg < HG; ++hg) {
-#pragma unroll
-      for (int nb = 0; nb < NB; ++nb) O[hg][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
-      m_seen[hg] = kNoRef;
-      l_lane[hg] = 0.f;
-      Ph[hg] = Pl[hg] = u32x4{0u, 0u, 0u, 0u};
-    }
-    // the window rows go to wave 0's buffer before any tile load is issued
-    // (the barrier waits for every load in flight)
-    u32x4 rp[2][KR];
-    if (win_block) {
-      __syncthreads();  // wave 0's buffer is free (zeroed, or done with the last pass)
-      stage_window();
-      if (win_mine) window_rope(rp);
-      __syncthreads();
-    }
-    bool first = pass == 0;
-    if (win_mine) {
-      window_tile(rp, first);
-      first = false;
-    }
-    // Tile pipeline: tile i + 1's data is loaded into dn while tile i is
-    // computed from dc, and the pages are looked up a tile before that. The
-    // loop is not unrolled (the copy dc = dn costs 36 moves per tile): with
-    // unrolled register slots the allocator spills, and four independent waves
-    // per CU keep enough bytes in flight with one tile of prefetch each. The
-    // scheduling barriers keep the issue order, so the compiler's counted
-    // waits release tile i while tile i + 1's loads are in flight.
-    const int nl = n - 1;
-    if (n > 0) {
+    if (pass > 0) init_pass();
+    // Tile pipeline: two register slots (dn, dc) take turns, unrolled by two
+    // so that no tile is copied between them: tile i + 1's data is loaded
+    // into one slot while tile i is computed from the other, and the pages are
+    // looked up a tile before that (the first pass's first tile is already in
+    // flight from the prologue). Four independent waves per CU keep enough
+    // bytes in flight with one tile of prefetch each. The scheduling barriers
+    // keep the issue order, so the compiler's counted waits release tile i
+    // while tile i + 1's loads are in flight.
+    if (pass > 0 && n > 0) {
       lookup(0, pgc);
       lookup(min(1, nl), pgn);
       __builtin_amdgcn_sched_barrier(0);
       load(0, pgc, dn);
       __builtin_amdgcn_sched_barrier(0);
     }
-    for (int i = 0; i < n; ++i) {
-      dc = dn;  // tile i
+    bool first = pass == 0;
+    if (win_mine) {
+      window_tile(first);
+      first = false;
+    }
+    int i = 0;
+    for (; i + 1 < n; i += 2) {
+      // tile i is in dn: load tile i + 1 into dc, compute tile i
       pgc[0] = pgn[0];
       pgc[1] = pgn[1];
       __builtin_amdgcn_sched_barrier(0);
-      load(min(i + 1, nl), pgc, dn);
+      load(i + 1, pgc, dc);
       __builtin_amdgcn_sched_barrier(0);
       lookup(min(i + 2, nl), pgn);
       __builtin_amdgcn_sched_barrier(0);
-      compute(i, dc, first);
+      compute(i, dn, first);
+      first = false;
+      // tile i + 1 is in dc: load tile i + 2 into dn, compute tile i + 1
+      pgc[0] = pgn[0];
+      pgc[1] = pgn[1];
+      __builtin_amdgcn_sched_barrier(0);
+      load(min(i + 2, nl), pgc, dn);
+      __builtin_amdgcn_sched_barrier(0);
+      lookup(min(i + 3, nl), pgn);
+      __builtin_amdgcn_sched_barrier(0);
+      compute(i + 1, dc, false);
+    }
+    if (i < n) {
+      compute(i, dn, first);  // the last tile (odd count), already in dn
       first = false;
     }
     flush();
@@ -591,35 +609,36 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
   float* const mbuf = reinterpret_cast<float*>(wbuf);  // this wave's O, [16 heads][D] in LDS element order
 #pragma unroll
   for (int hg = 0; hg < HG; ++hg) {
-    // this wave's weight for head la: exp2(m_w - M) / sum_w' exp2(m_w' - M) l_w'
-    float M = kNoRef;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, s_m[w][hg][la]);
-    float Ls = 0.f;
-#pragma unroll
-    for (int w = 0; w < kWaves; ++w) Ls += __builtin_amdgcn_exp2f(s_m[w][hg][la] - M) * s_l[w][hg][la];
-    const float fac = Ls > 0.f ? __builtin_amdgcn_exp2f(s_m[wave][hg][la] - M) / Ls : 0.f;
-    float fr[4];
-#pragma unroll
-    for (int r = 0; r < 4; ++r) fr[r] = __shfl(fac, 4 * gq + r);  // O rows are heads 4gq + r
+    // each wave's raw O (weighted in the sum below, so the accumulators go
+    // to LDS straight from their registers)
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) mbuf[(4 * gq + r) * D + 16 * nb + la] = O[hg][nb][r] * fr[r];
+      for (int r = 0; r < 4; ++r) mbuf[(4 * gq + r) * D + 16 * nb + la] = O[hg][nb][r];
     __syncthreads();
-    // sum of the four waves; LDS element 32j + 8gq' + i of a row is feature
-    // feature(gq', j, pi(i)), so 8 consecutive elements are 8 consecutive
-    // features in pi order
+    // sum of the four waves, wave w weighted by exp2(m_w - M) / sum_w' exp2(m_w' - M) l_w';
+    // LDS element 32j + 8gq' + i of a row is feature feature(gq', j, pi(i)),
+    // so 8 consecutive elements are 8 consecutive features in pi order
     for (int e = tid; e < 16 * D / 8; e += kThreads) {
       const int h = e / (D / 8), oct = e % (D / 8);
       const int j = oct / 4, gqo = oct % 4;
       const int f0 = 128 * lane_group<D>(gqo) + 16 * (lane_word0<D>(gqo) + j / 2) + 8 * (j & 1);
+      float M = kNoRef, Ls = 0.f, wt[kWaves];
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) M = fmaxf(M, s_m[w][hg][h]);
+#pragma unroll
+      for (int w = 0; w < kWaves; ++w) {
+        wt[w] = __builtin_amdgcn_exp2f(s_m[w][hg][h] - M);
+        Ls += wt[w] * s_l[w][hg][h];
+      }
+      const float inv = Ls > 0.f ? 1.f / Ls : 0.f;
       f32x4 lo4 = {0.f, 0.f, 0.f, 0.f}, hi4 = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int w = 0; w < kWaves; ++w) {
         const float* src = reinterpret_cast<const float*>(s_buf + w * G::WBUF) + h * D + 8 * oct;
-        lo4 += *reinterpret_cast<const f32x4*>(src);
-        hi4 += *reinterpret_cast<const f32x4*>(src + 4);
+        const float f = wt[w] * inv;
+        lo4 += *reinterpret_cast<const f32x4*>(src) * f;
+        hi4 += *reinterpret_cast<const f32x4*>(src + 4) * f;
       }
       const int hh = 16 * hg + h;
       if (hh < nh) {
