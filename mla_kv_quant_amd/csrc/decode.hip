@@ -605,7 +605,9 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
       s_l[wave][hg][la] = l_sum[hg];
     }
   }
-  __syncthreads();  // every wave is done with its tile buffer
+  // (no barrier yet: each wave's buffer is its own until the sum below, and
+  // its own reads of it are done, so a wave stores its O as soon as it is
+  // finished while slower waves still run)
   float* const mbuf = reinterpret_cast<float*>(wbuf);  // this wave's O, [16 heads][D] in LDS element order
 #pragma unroll
   for (int hg = 0; hg < HG; ++hg) {
