@@ -19,6 +19,8 @@
 #include "rolaq_common.h"
 #include "rolaq_args.h"
 
+#include <cstddef>
+
 namespace rolaq {
 
 constexpr int kWriterWaves = 8;   // waves per block: two per SIMD, so one's epilogue overlaps the other's MFMAs
@@ -78,6 +80,16 @@ __device__ __forceinline__ u32x4 rms_apply8(u32x4 v, float r, u32x4 gm) {
   return o;
 }
 
+
+// A field of the kernel's WriterArgs argument, loaded from the kernel argument
+// segment where it is used (the argument sits at offset 0).
+template <typename T>
+__device__ __forceinline__ T kernarg_field(size_t off) {
+  const auto k = (const __attribute__((address_space(4))) char*)__builtin_amdgcn_kernarg_segment_ptr();
+  T v = *(const __attribute__((address_space(4))) T*)(k + off);
+  asm volatile("" : "+s"(v));  // not merged with the argument's first load
+  return v;
+}
 
 template <int D>
 struct WriterGeo {
@@ -262,11 +274,20 @@ __global__ __launch_bounds__(64 * kWriterWaves, 1) void writer_kernel(WriterArgs
     }
 
     // ---- epilogue: lane (la, gq) holds columns 32gq..32gq+31 of row 16nb+la ---
+    // The lane's row within the tile, recomputed here: kept from the kernel's
+    // start, the compiler spills it, and every reload waits for all loads in
+    // flight (the next tile's latent rows among them).
+    int lane_now;
+    asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(lane_now));
+    const int lr = lane_now & 15, gr = lane_now >> 4;
     int64_t slot[4];
     int32_t seq[4], pos[4], req[4];
+    u32x2 pes[4];
 #pragma unroll
     for (int nb = 0; nb < 4; ++nb) {
-      const int64_t r = min(row0 + 16 * nb + la, a.n - 1);
+      const int64_t r = min(row0 + 16 * nb + lr, a.n - 1);
+      pes[nb] = a.pe_vec ? *reinterpret_cast<const u32x2*>(a.k_pe + r * a.pe_s0 + 16 * g + 4 * gr) : u32x2{0u, 0u};
+
       slot[nb] = a.loc[r];
       seq[nb] = seq32[2 * r];
       pos[nb] = pos32[2 * r] + pos_adj;
@@ -278,10 +299,9 @@ __global__ __launch_bounds__(64 * kWriterWaves, 1) void writer_kernel(WriterArgs
 #pragma unroll
     for (int nb = 0; nb < 4; ++nb) {
       __builtin_amdgcn_sched_barrier(0);
-      const int64_t row = row0 + 16 * nb + la;
+      const int64_t row = row0 + 16 * nb + lr;
       // rope columns [16 g, 16 g + 16) of the row, four per lane
-      u32x2 pe = {0u, 0u};
-      if (a.pe_vec) pe = *reinterpret_cast<const u32x2*>(a.k_pe + min(row, a.n - 1) * a.pe_s0 + 16 * g + 4 * gq);
+      const u32x2 pe = pes[nb];
       const bool live = row < a.n;
       const int64_t sl = slot[nb];
       // window bookkeeping (mla_fused_writer.py:36-51)
@@ -339,7 +359,10 @@ __global__ __launch_bounds__(64 * kWriterWaves, 1) void writer_kernel(WriterArgs
         }
         if (sl > 0) {
           if (a.pe_vec) {
-            *reinterpret_cast<u32x2*>(a.rope + sl * a.R + 16 * g + 4 * gq) = pe;
+            // the rope pool's base read again from the kernel arguments here
+            // (a scalar load), not held in a register that would be spilled
+            uint16_t* const rope = kernarg_field<uint16_t*>(offsetof(WriterArgs, rope));
+            *reinterpret_cast<u32x2*>(rope + sl * a.R + 16 * g + 4 * gr) = pe;
           } else if (g == 0) {
             for (int r = gq; r < a.R; r += 4) a.rope[sl * a.R + r] = a.k_pe[row * a.pe_s0 + r * a.pe_s1];
           }
