@@ -17,14 +17,15 @@
 //           once per call instead of once per query block.
 //   attend  a block takes BM consecutive (token, head) query rows of one
 //           sequence (all heads share the keys: MQA) and walks its keys in
-//           tiles of 32, each copied from the workspace into LDS by the whole
-//           block while the previous tile is consumed (double-buffered). Per
-//           wave and tile:
-//   S^T[32 keys, RW rows] = K . Q^T   on MFMA 16x16x32 (Q held in registers)
+//           tiles of 64, each copied from the workspace into LDS by the whole
+//           block while the previous tile is consumed (double-buffered, one
+//           barrier per tile). Per wave and tile:
+//   S^T[64 keys, RW rows] = K . Q^T   on MFMA 16x16x32 (Q held in registers);
+//   the causal mask only on tiles that reach past the block's first query position
 //   softmax in the log2 domain against a fixed per-row reference (the row's
 //   maximum over the first tile); a block whose scores exceed it by more than
 //   2^64 somewhere is redone with the true maxima, so O is never rescaled
-//   O[RW rows, D] += P . V           on MFMA 16x16x32, the keys of each lane
+//   O[RW rows, D] += P . V           on MFMA 16x16x32 per 32-key half, the keys of each lane
 //                                     taken in the order the score MFMA left them,
 //                                     P split into bf16 hi + lo (FP32-level accuracy).
 #include "rolaq_common.h"
@@ -32,7 +33,9 @@
 
 namespace rolaq {
 
-constexpr int kExtKeys = 32;          // keys per tile
+constexpr int kExtKeys = 64;          // keys per tile
+constexpr int kExtMK = kExtKeys / 16;  // 16-key blocks per tile
+constexpr int kExtKH = kExtKeys / 32;  // 32-key halves (K-steps of the output MFMA)
 constexpr float kExtSlack = 64.0f;    // log2 headroom of a score over the softmax reference
 constexpr float kExtMasked = -1.0e30f;
 
@@ -199,6 +202,7 @@ __global__ __launch_bounds__((64 * ExtGeo<D, R>::WAVES), 1) void extend_kernel(E
   }
 
   const float c2 = a.sm_scale * kLog2e;
+  const int qfirst = (int)(prefix + r0 / a.H);  // causal limit of the block's first row
   int qp[NBR];  // causal limit of each lane's rows (-1: no row)
 #pragma unroll
   for (int nb = 0; nb < NBR; ++nb) qp[nb] = (int)qpos[nb];
@@ -226,15 +230,15 @@ __global__ __launch_bounds__((64 * ExtGeo<D, R>::WAVES), 1) void extend_kernel(E
       if (it + 1 < ntiles) load_keys(k0 + kExtKeys);
 
       // ---- scores S^T[key, row] --------------------------------------------
-      f32x4 s[2][NBR];
+      f32x4 s[kExtMK][NBR];
 #pragma unroll
-      for (int mk = 0; mk < 2; ++mk)
+      for (int mk = 0; mk < kExtMK; ++mk)
 #pragma unroll
         for (int nb = 0; nb < NBR; ++nb) s[mk][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int ks = 0; ks < KSQ; ++ks) {
 #pragma unroll
-        for (int mk = 0; mk < 2; ++mk) {
+        for (int mk = 0; mk < kExtMK; ++mk) {
           const u32x4 kf = *reinterpret_cast<const u32x4*>(kb + (16 * mk + la) * G::KSTR + 64 * ks + 16 * gq);
 #pragma unroll
           for (int nb = 0; nb < NBR; ++nb) s[mk][nb] = mfma16x16x32(kf, qf[nb][ks], s[mk][nb]);
@@ -242,15 +246,17 @@ __global__ __launch_bounds__((64 * ExtGeo<D, R>::WAVES), 1) void extend_kernel(E
       }
 
       // ---- softmax against the fixed reference (row = 16 nb + la; keys 16 mk + 4 gq + i)
+      // A tile that ends before the block's first query position needs no mask.
+      const bool open = k0 + kExtKeys - 1 <= qfirst;
 #pragma unroll
       for (int nb = 0; nb < NBR; ++nb) {
         float mx = m_lane[nb];
 #pragma unroll
-        for (int mk = 0; mk < 2; ++mk)
+        for (int mk = 0; mk < kExtMK; ++mk)
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int kp = k0 + 16 * mk + 4 * gq + i;
-            const float v = kp <= qp[nb] ? s[mk][nb][i] * c2 : kExtMasked;
+            const float v = (open || kp <= qp[nb]) ? s[mk][nb][i] * c2 : kExtMasked;
             s[mk][nb][i] = v;
             mx = fmaxf(mx, v);
           }
@@ -262,7 +268,9 @@ __global__ __launch_bounds__((64 * ExtGeo<D, R>::WAVES), 1) void extend_kernel(E
 #pragma unroll
         for (int nb = 0; nb < NBR; ++nb) m_ref[nb] = max_over_rows(m_lane[nb]);
       }
-      u32x4 pf[NBR], pl[NBR];
+      u32x4 pf[kExtKH][NBR], pl[kExtKH][NBR];
+#pragma unroll
+      for (int kh = 0; kh < kExtKH; ++kh)
 #pragma unroll
       for (int nb = 0; nb < NBR; ++nb) {
         float p[2][4];
@@ -270,32 +278,35 @@ __global__ __launch_bounds__((64 * ExtGeo<D, R>::WAVES), 1) void extend_kernel(E
         for (int mk = 0; mk < 2; ++mk)
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            p[mk][i] = __builtin_amdgcn_exp2f(s[mk][nb][i] - m_ref[nb]);  // masked: 2^-1e30 = 0
+            p[mk][i] = __builtin_amdgcn_exp2f(s[2 * kh + mk][nb][i] - m_ref[nb]);  // masked: 2^-1e30 = 0
             l_run[nb] += p[mk][i];
           }
         // P as bf16 hi + lo: the output keeps FP32-level accuracy in P
-        pf[nb] = u32x4{pack_bf16(p[0][0], p[0][1]), pack_bf16(p[0][2], p[0][3]), pack_bf16(p[1][0], p[1][1]),
-                       pack_bf16(p[1][2], p[1][3])};
+        pf[kh][nb] = u32x4{pack_bf16(p[0][0], p[0][1]), pack_bf16(p[0][2], p[0][3]), pack_bf16(p[1][0], p[1][1]),
+                           pack_bf16(p[1][2], p[1][3])};
         float r[2][4];
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const uint32_t w = pf[nb][e];
+          const uint32_t w = pf[kh][nb][e];
           r[e >> 1][2 * (e & 1)] = p[e >> 1][2 * (e & 1)] - bf16_lo(w);
           r[e >> 1][2 * (e & 1) + 1] = p[e >> 1][2 * (e & 1) + 1] - bf16_hi(w);
         }
-        pl[nb] = u32x4{pack_bf16(r[0][0], r[0][1]), pack_bf16(r[0][2], r[0][3]), pack_bf16(r[1][0], r[1][1]),
-                       pack_bf16(r[1][2], r[1][3])};
+        pl[kh][nb] = u32x4{pack_bf16(r[0][0], r[0][1]), pack_bf16(r[0][2], r[0][3]), pack_bf16(r[1][0], r[1][1]),
+                           pack_bf16(r[1][2], r[1][3])};
       }
 
       // ---- O[row, d] += P . V ------------------------------------------------
 #pragma unroll
+      for (int kh = 0; kh < kExtKH; ++kh)
+#pragma unroll
       for (int nd = 0; nd < ND; ++nd) {
-        const u32x2 v0 = read_v_tr(kb, G::KSTR, gq, la, nd, 0), v1 = read_v_tr(kb, G::KSTR, gq, la, nd, 1);
+        const uint8_t* kv = kb + 32 * kh * G::KSTR;
+        const u32x2 v0 = read_v_tr(kv, G::KSTR, gq, la, nd, 0), v1 = read_v_tr(kv, G::KSTR, gq, la, nd, 1);
         const u32x4 vf = {v0.x, v0.y, v1.x, v1.y};
 #pragma unroll
         for (int nb = 0; nb < NBR; ++nb) {
-          acc_o[nb][nd] = mfma16x16x32(pf[nb], vf, acc_o[nb][nd]);
-          acc_o[nb][nd] = mfma16x16x32(pl[nb], vf, acc_o[nb][nd]);
+          acc_o[nb][nd] = mfma16x16x32(pf[kh][nb], vf, acc_o[nb][nd]);
+          acc_o[nb][nd] = mfma16x16x32(pl[kh][nb], vf, acc_o[nb][nd]);
         }
       }
 
