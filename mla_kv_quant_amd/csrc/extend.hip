@@ -246,7 +246,8 @@ __global__ __launch_bounds__((64 * ExtGeo<D, R>::WAVES), 1) void extend_kernel(E
       }
 
       // ---- softmax against the fixed reference (row = 16 nb + la; keys 16 mk + 4 gq + i)
-      // A tile that ends before the block's first query position needs no mask.
+      // A tile that ends before the block's first query position needs no mask
+      // (rows past the last query, qp = -1, stay masked: no scores, no redo).
       const bool open = k0 + kExtKeys - 1 <= qfirst;
 #pragma unroll
       for (int nb = 0; nb < NBR; ++nb) {
@@ -256,7 +257,7 @@ __global__ __launch_bounds__((64 * ExtGeo<D, R>::WAVES), 1) void extend_kernel(E
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int kp = k0 + 16 * mk + 4 * gq + i;
-            const float v = (open || kp <= qp[nb]) ? s[mk][nb][i] * c2 : kExtMasked;
+            const float v = ((open && qp[nb] >= 0) || kp <= qp[nb]) ? s[mk][nb][i] * c2 : kExtMasked;
             s[mk][nb][i] = v;
             mx = fmaxf(mx, v);
           }
