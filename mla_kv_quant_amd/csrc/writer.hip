@@ -361,8 +361,11 @@ __global__ __launch_bounds__(64 * kWriterWaves, 1) void writer_kernel(WriterArgs
           if (a.pe_vec) {
             // the rope pool's base read again from the kernel arguments here
             // (a scalar load), not held in a register that would be spilled
+            // (as a global pointer: through a generic one the store is a flat
+            // store, which the next LDS waits would also wait for)
+            typedef __attribute__((address_space(1))) u32x2 g_u32x2;
             uint16_t* const rope = kernarg_field<uint16_t*>(offsetof(WriterArgs, rope));
-            *reinterpret_cast<u32x2*>(rope + sl * a.R + 16 * g + 4 * gr) = pe;
+            *(g_u32x2*)(rope + sl * a.R + 16 * g + 4 * gr) = pe;
           } else if (g == 0) {
             for (int r = gq; r < a.R; r += 4) a.rope[sl * a.R + r] = a.k_pe[row * a.pe_s0 + r * a.pe_s1];
           }
