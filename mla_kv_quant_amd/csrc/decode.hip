@@ -418,23 +418,29 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
       t[mb] = make_lut(d.prm[mb], pos >= lo && pos < hi);
     }
     // Word step s: the expansion of step s, the output MFMAs of step s on the
-    // reads issued in the previous step, the stores of step s, its score
-    // MFMAs, then the reads of step s + 1. Step s stores over the elements its
-    // reads came from, so it first waits for them (issued a step earlier, the
-    // wait is normally free). The scheduling groups interleave the output
-    // MFMAs with the expansion's VALU work, so the matrix core runs while the
-    // VALU expands, and the score MFMAs with the next reads.
-    u32x2 vr[2][4][2];
+    // reads issued PFD steps earlier, the stores of step s, its score MFMAs,
+    // then the reads of step s + PFD. Step s stores over the elements its
+    // reads came from; the LDS runs a wave's instructions in order, so those
+    // reads (issued earlier) have their data before the stores land, and the
+    // only waits are the compiler's, for the read registers. The scheduling
+    // groups interleave the output MFMAs with the expansion's VALU work, so
+    // the matrix core runs while the VALU expands, and the score MFMAs with
+    // the next reads. Reads two steps ahead give them a whole step of cover
+    // (one step with three head groups, whose registers are full).
+    constexpr int PFD = HG >= 3 ? 1 : 2;  // steps the transposed reads run ahead
+    u32x2 vr[PFD + 1][4][2];
 #pragma unroll
     for (int k = 0; k < 4; ++k)
 #pragma unroll
-      for (int h = 0; h < 2; ++h) vr[0][k][h] = vt_read(k, h);
+      for (int h = 0; h < 2; ++h) {
+        vr[0][k][h] = vt_read(k, h);
+        if (PFD > 1 && WPL > 1) vr[1][k][h] = vt_read(4 + k, h);
+      }
     __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int s = 0; s < WPL; ++s) {
-      u32x2 (&cur)[4][2] = vr[s & 1];
-      u32x2 (&nxt)[4][2] = vr[(s + 1) & 1];
-      __builtin_amdgcn_s_waitcnt(kLgkmcnt0);  // step s's reads are back
+      u32x2 (&cur)[4][2] = vr[s % (PFD + 1)];
+      u32x2 (&nxt)[4][2] = vr[(s + PFD) % (PFD + 1)];
       asm volatile("" ::: "memory");
       u32x4 c[2][2];
 #pragma unroll
@@ -453,11 +459,11 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
           S[mb][hg] = mfma16x16x32(c[mb][0], qB[hg][2 * s], S[mb][hg]);
           So[mb][hg] = mfma16x16x32(c[mb][1], qB[hg][2 * s + 1], So[mb][hg]);
         }
-      if (s + 1 < WPL) {
+      if (s + PFD < WPL) {
 #pragma unroll
         for (int k = 0; k < 4; ++k)
 #pragma unroll
-          for (int h = 0; h < 2; ++h) nxt[k][h] = vt_read(4 * (s + 1) + k, h);
+          for (int h = 0; h < 2; ++h) nxt[k][h] = vt_read(4 * (s + PFD) + k, h);
       }
       // issue order: (5 VALU, HG output MFMAs) x 8, the rest of the VALU,
       // the stores, then (HG score MFMAs, 2 reads) x 4
