@@ -19,22 +19,30 @@
 // own softmax state, holding the query of HG head groups in registers. Per
 // 32-token tile:
 //   expansion  a lane owns one (token, quantization group): the four levels
-//              bf16((k - zero) * scale), k = 0..3, form a byte table, and two
-//              byte permutes per four codes pick the lanes' bf16 values, which
-//              ARE the reference's stored row (no approximation);
-//   scores     S^T[token, head] = K Q^T on bf16 MFMA 16x16x32 with the
-//              expanded codes as the A operand in registers (exact products,
-//              FP32 accumulate), rope likewise;
-//   softmax    FP32 in the log2 domain against a fixed per-wave reference
-//              (the first tile's maximum; a block where a score exceeds it by
-//              more than 2^64 is redone with the true maxima);
-//   output     O[head, f] += P V on bf16 MFMA with P as a bf16 hi + lo pair
-//              (FP32-level accuracy) and V read transposed out of the wave's
-//              LDS copy of the expanded tile (ds_read_b64_tr_b16).
+//              bf16((k - zero) * scale), k = 0..3, carried as fp16 (the same
+//              numbers: a bf16 value is exact in fp16 between 2^-17 and
+//              65504), form a byte table, and two byte permutes per four
+//              codes pick the lanes' values, which ARE the reference's stored
+//              row (no approximation);
+//   scores     S^T[token, head] = K Q^T on fp16 MFMA 16x16x32 with the
+//              expanded codes as the A operand in registers and the latent
+//              query converted to fp16 once (exact products, FP32
+//              accumulate); rope on bf16 MFMA into the same accumulators;
+//   softmax    FP32 in the log2 domain against a per-wave reference per head
+//              (the first tile's maximum); a tile whose maximum passes it by
+//              more than 15 moves it there and scales O and the sum by the
+//              difference, so every probability is at most 2^15;
+//   output     O[head, f] += P V on fp16 MFMA (P rounded to fp16: relative
+//              error 2^-12 per probability) with V read transposed out of the
+//              wave's LDS copy of the expanded tile (ds_read_b64_tr_b16).
 // The output contraction of a tile runs inside the next tile's expansion
 // (both touch the same LDS elements, old reads before new writes). Loads go
 // straight to registers, one tile ahead; the four waves merge their (max,
 // sum, O) through LDS into one partial per block.
+//
+// Range: the latent query, the stored INT2 levels and the window rows are
+// carried in fp16, so magnitudes above 65504 become inf and the outputs of
+// that request non-finite (never silently wrong); rope terms stay bf16.
 #include "rolaq_common.h"
 #include "rolaq_args.h"
 
@@ -47,7 +55,8 @@ constexpr int kWaves = 4;                  // one per SIMD
 constexpr int kThreads = 64 * kWaves;
 constexpr int kXcds = 8;                   // accelerator dies (own L2 each) of the MI355X
 constexpr float kNoRef = -1.0e30f;         // masked score / "no score yet" (log2 units)
-constexpr float kRefSlack = 64.f;          // max exp2 argument before a block is redone
+constexpr float kRefSlack = 15.f;          // max exp2 argument: a probability stays <= 2^15 (fp16)
+constexpr float kRefHeadroom = 8.f;        // a reference sits this far above the maximum it was set from
 // instruction classes of __builtin_amdgcn_sched_group_barrier
 constexpr int kSchedValu = 0x002, kSchedMfma = 0x008, kSchedDsRead = 0x100, kSchedDsWrite = 0x200;
 // s_waitcnt immediate (gfx9 encoding) waiting for lgkmcnt == 0 only
@@ -69,7 +78,7 @@ struct DGeo {
 
 // ---------------------------------------------------------------------------
 // Expanded-row layout in LDS. Lane (la, gq) of the score MFMA at K-step j
-// holds 8 bf16 of token la: features feature(gq, j, i), i = 0..7, stored as the
+// holds 8 fp16 of token la: features feature(gq, j, i), i = 0..7, stored as the
 // 16-byte logical chunk 4j + gq of the token's row, so a row's LDS element
 // e = 32j + 8gq + i. Physical chunk = logical ^ sw(row): the 8 rows that a
 // 16-byte store of 8 lanes touches, and the 4 rows x 2 chunks that a 16-lane
@@ -92,25 +101,26 @@ __device__ __forceinline__ u32x4 pi_permute(u32x4 n) {
                __builtin_amdgcn_perm(n.w, n.y, 0x05040100u), __builtin_amdgcn_perm(n.w, n.y, 0x07060302u)};
 }
 
-// Byte tables of the four stored levels v_k = bf16((k - zero) * scale):
-// L = low bytes of v_0..v_3, H = high bytes. A masked token gets zeros.
+// Byte tables of the four stored levels v_k = bf16((k - zero) * scale), as
+// fp16: L = low bytes of v_0..v_3, H = high bytes. A masked token gets zeros.
 struct Lut {
   uint32_t L, H;
 };
 __device__ __forceinline__ Lut make_lut(f32x2 sz, bool live) {
   const float s = sz.x, z = sz.y;
-  const uint32_t A = pack_bf16((0.0f - z) * s, (1.0f - z) * s);
-  const uint32_t B = pack_bf16((2.0f - z) * s, (3.0f - z) * s);
+  const uint32_t A = bf16x2_to_f16x2(pack_bf16((0.0f - z) * s, (1.0f - z) * s));
+  const uint32_t B = bf16x2_to_f16x2(pack_bf16((2.0f - z) * s, (3.0f - z) * s));
   Lut t;
   t.L = live ? __builtin_amdgcn_perm(B, A, 0x06040200u) : 0u;
   t.H = live ? __builtin_amdgcn_perm(B, A, 0x07050301u) : 0u;
   return t;
 }
 
-// One packed word (16 codes, code p at bits 2p) -> two 16-byte chunks of bf16:
-// c0 = features [0,4,1,5,2,6,3,7], c1 = 8 + the same. x_p selects, per byte,
-// the codes p, p+4, p+8, p+12; a permute with the code bytes as selectors
-// reads the tables; two more interleave low and high bytes into bf16 pairs.
+// One packed word (16 codes, code p at bits 2p) -> two 16-byte chunks of
+// 16-bit values: c0 = features [0,4,1,5,2,6,3,7], c1 = 8 + the same. x_p
+// selects, per byte, the codes p, p+4, p+8, p+12; a permute with the code
+// bytes as selectors reads the tables; two more interleave low and high bytes
+// into value pairs.
 __device__ __forceinline__ void expand_word(uint32_t w, const Lut& t, u32x4& c0, u32x4& c1) {
   uint32_t lo[4], hi[4];
 #pragma unroll
@@ -124,6 +134,202 @@ __device__ __forceinline__ void expand_word(uint32_t w, const Lut& t, u32x4& c0,
     c0[p] = __builtin_amdgcn_perm(hi[p], lo[p], 0x05010400u);
     c1[p] = __builtin_amdgcn_perm(hi[p], lo[p], 0x07030602u);
   }
+}
+
+// In-place scaling of an output accumulator held in an AGPR tuple. The
+// compiler prints an "a" operand of four floats as a[b:b+3]; the assembler
+// macro ROLAQ_ACC_BASE recovers b by comparing that text with every even base
+// (an operand anywhere else stops the assembly with an error), so that
+// ROLAQ_ACC_SCALE can read, scale and write the four registers one by one
+// (v_accvgpr_read / v_mul_f32 / v_accvgpr_write) without the compiler ever
+// seeing the accumulators leave their registers. Inline asm blobs share one
+// assembler state in order of emission, so the definitions are made once, at
+// the start of each kernel.
+#define ROLAQ_ACC_CASE(k, k3) "  .ifc \\t, a[" #k ":" #k3 "]\n    .set rolaq_acc_b, " #k "\n  .endif\n"
+#define ROLAQ_ACC_CASES \
+  ROLAQ_ACC_CASE(0, 3) \
+  ROLAQ_ACC_CASE(2, 5) \
+  ROLAQ_ACC_CASE(4, 7) \
+  ROLAQ_ACC_CASE(6, 9) \
+  ROLAQ_ACC_CASE(8, 11) \
+  ROLAQ_ACC_CASE(10, 13) \
+  ROLAQ_ACC_CASE(12, 15) \
+  ROLAQ_ACC_CASE(14, 17) \
+  ROLAQ_ACC_CASE(16, 19) \
+  ROLAQ_ACC_CASE(18, 21) \
+  ROLAQ_ACC_CASE(20, 23) \
+  ROLAQ_ACC_CASE(22, 25) \
+  ROLAQ_ACC_CASE(24, 27) \
+  ROLAQ_ACC_CASE(26, 29) \
+  ROLAQ_ACC_CASE(28, 31) \
+  ROLAQ_ACC_CASE(30, 33) \
+  ROLAQ_ACC_CASE(32, 35) \
+  ROLAQ_ACC_CASE(34, 37) \
+  ROLAQ_ACC_CASE(36, 39) \
+  ROLAQ_ACC_CASE(38, 41) \
+  ROLAQ_ACC_CASE(40, 43) \
+  ROLAQ_ACC_CASE(42, 45) \
+  ROLAQ_ACC_CASE(44, 47) \
+  ROLAQ_ACC_CASE(46, 49) \
+  ROLAQ_ACC_CASE(48, 51) \
+  ROLAQ_ACC_CASE(50, 53) \
+  ROLAQ_ACC_CASE(52, 55) \
+  ROLAQ_ACC_CASE(54, 57) \
+  ROLAQ_ACC_CASE(56, 59) \
+  ROLAQ_ACC_CASE(58, 61) \
+  ROLAQ_ACC_CASE(60, 63) \
+  ROLAQ_ACC_CASE(62, 65) \
+  ROLAQ_ACC_CASE(64, 67) \
+  ROLAQ_ACC_CASE(66, 69) \
+  ROLAQ_ACC_CASE(68, 71) \
+  ROLAQ_ACC_CASE(70, 73) \
+  ROLAQ_ACC_CASE(72, 75) \
+  ROLAQ_ACC_CASE(74, 77) \
+  ROLAQ_ACC_CASE(76, 79) \
+  ROLAQ_ACC_CASE(78, 81) \
+  ROLAQ_ACC_CASE(80, 83) \
+  ROLAQ_ACC_CASE(82, 85) \
+  ROLAQ_ACC_CASE(84, 87) \
+  ROLAQ_ACC_CASE(86, 89) \
+  ROLAQ_ACC_CASE(88, 91) \
+  ROLAQ_ACC_CASE(90, 93) \
+  ROLAQ_ACC_CASE(92, 95) \
+  ROLAQ_ACC_CASE(94, 97) \
+  ROLAQ_ACC_CASE(96, 99) \
+  ROLAQ_ACC_CASE(98, 101) \
+  ROLAQ_ACC_CASE(100, 103) \
+  ROLAQ_ACC_CASE(102, 105) \
+  ROLAQ_ACC_CASE(104, 107) \
+  ROLAQ_ACC_CASE(106, 109) \
+  ROLAQ_ACC_CASE(108, 111) \
+  ROLAQ_ACC_CASE(110, 113) \
+  ROLAQ_ACC_CASE(112, 115) \
+  ROLAQ_ACC_CASE(114, 117) \
+  ROLAQ_ACC_CASE(116, 119) \
+  ROLAQ_ACC_CASE(118, 121) \
+  ROLAQ_ACC_CASE(120, 123) \
+  ROLAQ_ACC_CASE(122, 125) \
+  ROLAQ_ACC_CASE(124, 127) \
+  ROLAQ_ACC_CASE(126, 129) \
+  ROLAQ_ACC_CASE(128, 131) \
+  ROLAQ_ACC_CASE(130, 133) \
+  ROLAQ_ACC_CASE(132, 135) \
+  ROLAQ_ACC_CASE(134, 137) \
+  ROLAQ_ACC_CASE(136, 139) \
+  ROLAQ_ACC_CASE(138, 141) \
+  ROLAQ_ACC_CASE(140, 143) \
+  ROLAQ_ACC_CASE(142, 145) \
+  ROLAQ_ACC_CASE(144, 147) \
+  ROLAQ_ACC_CASE(146, 149) \
+  ROLAQ_ACC_CASE(148, 151) \
+  ROLAQ_ACC_CASE(150, 153) \
+  ROLAQ_ACC_CASE(152, 155) \
+  ROLAQ_ACC_CASE(154, 157) \
+  ROLAQ_ACC_CASE(156, 159) \
+  ROLAQ_ACC_CASE(158, 161) \
+  ROLAQ_ACC_CASE(160, 163) \
+  ROLAQ_ACC_CASE(162, 165) \
+  ROLAQ_ACC_CASE(164, 167) \
+  ROLAQ_ACC_CASE(166, 169) \
+  ROLAQ_ACC_CASE(168, 171) \
+  ROLAQ_ACC_CASE(170, 173) \
+  ROLAQ_ACC_CASE(172, 175) \
+  ROLAQ_ACC_CASE(174, 177) \
+  ROLAQ_ACC_CASE(176, 179) \
+  ROLAQ_ACC_CASE(178, 181) \
+  ROLAQ_ACC_CASE(180, 183) \
+  ROLAQ_ACC_CASE(182, 185) \
+  ROLAQ_ACC_CASE(184, 187) \
+  ROLAQ_ACC_CASE(186, 189) \
+  ROLAQ_ACC_CASE(188, 191) \
+  ROLAQ_ACC_CASE(190, 193) \
+  ROLAQ_ACC_CASE(192, 195) \
+  ROLAQ_ACC_CASE(194, 197) \
+  ROLAQ_ACC_CASE(196, 199) \
+  ROLAQ_ACC_CASE(198, 201) \
+  ROLAQ_ACC_CASE(200, 203) \
+  ROLAQ_ACC_CASE(202, 205) \
+  ROLAQ_ACC_CASE(204, 207) \
+  ROLAQ_ACC_CASE(206, 209) \
+  ROLAQ_ACC_CASE(208, 211) \
+  ROLAQ_ACC_CASE(210, 213) \
+  ROLAQ_ACC_CASE(212, 215) \
+  ROLAQ_ACC_CASE(214, 217) \
+  ROLAQ_ACC_CASE(216, 219) \
+  ROLAQ_ACC_CASE(218, 221) \
+  ROLAQ_ACC_CASE(220, 223) \
+  ROLAQ_ACC_CASE(222, 225) \
+  ROLAQ_ACC_CASE(224, 227) \
+  ROLAQ_ACC_CASE(226, 229) \
+  ROLAQ_ACC_CASE(228, 231) \
+  ROLAQ_ACC_CASE(230, 233) \
+  ROLAQ_ACC_CASE(232, 235) \
+  ROLAQ_ACC_CASE(234, 237) \
+  ROLAQ_ACC_CASE(236, 239) \
+  ROLAQ_ACC_CASE(238, 241) \
+  ROLAQ_ACC_CASE(240, 243) \
+  ROLAQ_ACC_CASE(242, 245) \
+  ROLAQ_ACC_CASE(244, 247) \
+  ROLAQ_ACC_CASE(246, 249) \
+  ROLAQ_ACC_CASE(248, 251) \
+  ROLAQ_ACC_CASE(250, 253) \
+  ROLAQ_ACC_CASE(252, 255)
+// Defines the macros for the rest of the assembly (each kernel calls it first;
+// the assembler keeps the definitions, and the guard skips a second one).
+__device__ __forceinline__ void define_acc_macros() {
+  asm volatile(
+    ".ifndef rolaq_acc_macros\n"
+    ".set rolaq_acc_macros, 1\n"
+    ".macro ROLAQ_ACC_BASE t\n"
+    "  .set rolaq_acc_b, -1\n" ROLAQ_ACC_CASES
+    "  .if rolaq_acc_b < 0\n"
+    "    .error \"ROLAQ_ACC_BASE: not an AGPR tuple\"\n"
+    "  .endif\n"
+    ".endm\n"
+    ".macro ROLAQ_ACC_SCALE t, t0, t1, t2, t3, f0, f1, f2, f3\n"
+    "  ROLAQ_ACC_BASE \\t\n"
+    "  v_accvgpr_read_b32 \\t0, a[rolaq_acc_b]\n"
+    "  v_accvgpr_read_b32 \\t1, a[rolaq_acc_b+1]\n"
+    "  v_accvgpr_read_b32 \\t2, a[rolaq_acc_b+2]\n"
+    "  v_accvgpr_read_b32 \\t3, a[rolaq_acc_b+3]\n"
+    "  s_nop 1\n"
+    "  v_mul_f32_e32 \\t0, \\t0, \\f0\n"
+    "  v_mul_f32_e32 \\t1, \\t1, \\f1\n"
+    "  v_mul_f32_e32 \\t2, \\t2, \\f2\n"
+    "  v_mul_f32_e32 \\t3, \\t3, \\f3\n"
+    "  s_nop 1\n"
+    "  v_accvgpr_write_b32 a[rolaq_acc_b], \\t0\n"
+    "  v_accvgpr_write_b32 a[rolaq_acc_b+1], \\t1\n"
+    "  v_accvgpr_write_b32 a[rolaq_acc_b+2], \\t2\n"
+    "  v_accvgpr_write_b32 a[rolaq_acc_b+3], \\t3\n"
+    ".endm\n"
+    ".endif\n");
+}
+#undef ROLAQ_ACC_CASES
+#undef ROLAQ_ACC_CASE
+
+// Four output accumulators, element j of each scaled by f_j in place when
+// need (a lane mask) is not 0. The branch is inside the asm: for the compiler
+// the accumulators flow through unchanged in their registers, so the rare
+// rescale adds no copies at a join. The leading waits cover the output MFMA
+// that last wrote them (tens of instructions earlier), the trailing ones an
+// MFMA that reads them next.
+__device__ __forceinline__ void scale_acc4(f32x4& a, f32x4& b, f32x4& c, f32x4& d, const float (&f)[4],
+                                           uint64_t need) {
+  float t0, t1, t2, t3;
+  asm volatile(
+      "s_cmp_lg_u64 %12, 0\n\t"
+      "s_cbranch_scc0 1f\n\t"
+      "s_nop 7\n\ts_nop 7\n\t"
+      "ROLAQ_ACC_SCALE %0, %4, %5, %6, %7, %8, %9, %10, %11\n\t"
+      "ROLAQ_ACC_SCALE %1, %4, %5, %6, %7, %8, %9, %10, %11\n\t"
+      "ROLAQ_ACC_SCALE %2, %4, %5, %6, %7, %8, %9, %10, %11\n\t"
+      "ROLAQ_ACC_SCALE %3, %4, %5, %6, %7, %8, %9, %10, %11\n\t"
+      "s_nop 7\n"
+      "1:"
+      : "+a"(a), "+a"(b), "+a"(c), "+a"(d), "=&v"(t0), "=&v"(t1), "=&v"(t2), "=&v"(t3)
+      : "v"(f[0]), "v"(f[1]), "v"(f[2]), "v"(f[3]), "s"(need)
+      : "scc");
 }
 
 __device__ __forceinline__ void lds_store128(uint8_t* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
@@ -173,6 +379,7 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
   static_assert(R % 32 == 0 && D % 256 == 0, "unsupported shape");
   static_assert(16 * D * 4 <= G::WBUF, "merge buffer of one wave (one head group at a time)");
 
+  define_acc_macros();
   __shared__ __attribute__((aligned(16))) uint8_t s_buf[kWaves * G::WBUF];
   __shared__ float s_m[kWaves][HG][16];  // per wave: softmax reference of each head
   __shared__ float s_l[kWaves][HG][16];  // per wave: sum of exponentials of each head
@@ -250,9 +457,7 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
 
   // ---- per-wave softmax state and accumulators ----------------------------------
   f32x4 O[HG][NB];
-  float m_ref[HG], m_seen[HG], l_lane[HG];
-#pragma unroll
-  for (int hg = 0; hg < HG; ++hg) m_ref[hg] = kNoRef;
+  float m_ref[HG], l_lane[HG];
 
   auto page_of = [&](int pos) { return gload<int32_t>(a.kv_indices + kv0 + (pos >> a.page_shift)); };
   auto lookup = [&](int i, int32_t (&pg)[2]) {
@@ -286,21 +491,18 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
   __builtin_amdgcn_sched_barrier(0);
 
   // while they are in flight: this wave's buffer starts as zeros (see the
-  // pending-output rule below), and the first pass's state
-  u32x4 Ph[HG], Pl[HG];
-  auto init_pass = [&]() {
+  // pending-output rule below), and the softmax state
+  u32x4 Ph[HG];  // the pending tile's probabilities (fp16)
 #pragma unroll
-    for (int hg = 0; hg < HG; ++hg) {
+  for (int hg = 0; hg < HG; ++hg) {
 #pragma unroll
-      for (int nb = 0; nb < NB; ++nb) O[hg][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
-      m_seen[hg] = kNoRef;
-      l_lane[hg] = 0.f;
-      Ph[hg] = Pl[hg] = u32x4{0u, 0u, 0u, 0u};
-    }
-  };
+    for (int nb = 0; nb < NB; ++nb) O[hg][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    m_ref[hg] = kNoRef;
+    l_lane[hg] = 0.f;
+    Ph[hg] = u32x4{0u, 0u, 0u, 0u};
+  }
 #pragma unroll
   for (int k = 0; k < G::WBUF / 1024; ++k) lds_store128(wbuf + 1024 * k + 16 * lane, u32x4{0u, 0u, 0u, 0u});
-  init_pass();
   __builtin_amdgcn_sched_barrier(0);
   if (n > 0) load(0, pgc, dn);
   __builtin_amdgcn_sched_barrier(0);
@@ -308,7 +510,7 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
   for (int hg = 0; hg < HG; ++hg) {
     const bool hv = h0 + 16 * hg + la < a.H;
 #pragma unroll
-    for (int j = 0; j < KL; ++j) qB[hg][j] = hv ? pi_permute(qB[hg][j]) : u32x4{0u, 0u, 0u, 0u};
+    for (int j = 0; j < KL; ++j) qB[hg][j] = hv ? bf16x8_to_f16x8(pi_permute(qB[hg][j])) : u32x4{0u, 0u, 0u, 0u};
 #pragma unroll
     for (int kr = 0; kr < KR; ++kr) qR[hg][kr] = hv ? qR[hg][kr] : u32x4{0u, 0u, 0u, 0u};
   }
@@ -318,47 +520,82 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
   // (LDS elements 64s..64s+63), then writes its own expanded chunks to those
   // same elements (LDS executes one wave's operations in order), so one buffer
   // per wave suffices and the reads' latency and the output MFMAs overlap the
-  // expansion's VALU work. Ph / Pl hold the pending tile's probabilities; at
-  // the start of a pass they are zero and the buffer holds finite values
-  // (zeros, or rows of the previous pass), so the first step's contraction
-  // adds exactly 0.
+  // expansion's VALU work. Ph holds the pending tile's probabilities; at
+  // the start they are zero and the buffer holds zeros, so the first step's
+  // contraction adds exactly 0.
 
-  // softmax of one tile (scores S, validity of token 16 mb + 4 gq + r) into Ph / Pl
-  auto softmax = [&](f32x4 (&S)[2][HG], auto valid, bool first) {
+  // Probabilities are 2^(score - reference) against a per-wave, per-head
+  // reference: the first tile's maximum + 8. A tile whose scores pass the
+  // reference by more than 15 (a probability would not fit fp16) moves the
+  // reference of those heads to its maximum + 8 and scales O and the sum by
+  // the difference, in place, before its probabilities are formed. The
+  // pending tile's output is already in O (its MFMAs ran inside this tile's
+  // steps). O's lane holds heads 4 gq + j (j = 0..3); their factors come from
+  // the lanes whose row la is that head.
+  auto rescale = [&](const float (&mx)[HG], const uint64_t (&need)[HG]) {
 #pragma unroll
     for (int hg = 0; hg < HG; ++hg) {
-      float x[8];
+      float fj[4] = {1.f, 1.f, 1.f, 1.f};
+      if (need[hg]) {
+        const float mt = wave_max_over_groups(mx[hg]);
+        const float mn = mt > m_ref[hg] + kRefSlack ? mt + kRefHeadroom : m_ref[hg];
+        const float f = __builtin_amdgcn_exp2f(m_ref[hg] - mn);  // 0 when nothing was summed yet
+        l_lane[hg] *= f;
+        m_ref[hg] = mn;
+#pragma unroll
+        for (int j = 0; j < 4; ++j) fj[j] = __shfl(f, 4 * gq + j);
+      }
+#pragma unroll
+      for (int nb = 0; nb < NB; nb += 4)
+        scale_acc4(O[hg][nb], O[hg][nb + 1], O[hg][nb + 2], O[hg][nb + 3], fj, need[hg]);
+    }
+  };
+  // the scores of one tile in log2 units, masked by the validity of token
+  // 16 mb + 4 gq + r
+  auto masked = [&](const f32x4 (&S)[2][HG], auto valid, float (&x)[HG][8]) {
+#pragma unroll
+    for (int hg = 0; hg < HG; ++hg)
 #pragma unroll
       for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
-        for (int r = 0; r < 4; ++r) x[4 * mb + r] = valid(16 * mb + 4 * gq + r) ? S[mb][hg][r] * sl2 : kNoRef;
-      float mx = x[0];
+        for (int r = 0; r < 4; ++r)
+          x[hg][4 * mb + r] = valid(16 * mb + 4 * gq + r) ? S[mb][hg][r] * sl2 : kNoRef;
+  };
+  // softmax of one tile's masked scores into Ph; the first tile of a wave sets
+  // the reference (nothing is summed yet). One instance per tile, so that O
+  // passes through one rescale on every path.
+  auto softmax = [&](const float (&x)[HG][8], bool first) {
+    float mx[HG];
+    uint64_t need[HG];  // per head group: lanes past the slack
 #pragma unroll
-      for (int i = 1; i < 8; ++i) mx = fmaxf(mx, x[i]);
-      m_seen[hg] = fmaxf(m_seen[hg], mx);
-      if (first) m_ref[hg] = wave_max_over_groups(mx);
+    for (int hg = 0; hg < HG; ++hg) {
+      mx[hg] = x[hg][0];
+#pragma unroll
+      for (int i = 1; i < 8; ++i) mx[hg] = fmaxf(mx[hg], x[hg][i]);
+      need[hg] = __builtin_amdgcn_ballot_w64(!first && mx[hg] > m_ref[hg] + kRefSlack);
+    }
+    if (first) {
+#pragma unroll
+      for (int hg = 0; hg < HG; ++hg) m_ref[hg] = wave_max_over_groups(mx[hg]) + kRefHeadroom;
+    }
+    rescale(mx, need);
+#pragma unroll
+    for (int hg = 0; hg < HG; ++hg) {
       float p[8], ls = 0.f;
 #pragma unroll
       for (int i = 0; i < 8; ++i) {
-        p[i] = __builtin_amdgcn_exp2f(x[i] - m_ref[hg]);  // masked: 2^-1e30 = 0
+        p[i] = __builtin_amdgcn_exp2f(x[hg][i] - m_ref[hg]);  // masked: 2^-1e30 = 0
         ls += p[i];
       }
       l_lane[hg] += ls;
 #pragma unroll
-      for (int d = 0; d < 4; ++d) {
-        const uint32_t hv = pack_bf16(p[2 * d], p[2 * d + 1]);
-        Ph[hg][d] = hv;
-        Pl[hg][d] = pack_bf16(p[2 * d] - bf16_lo(hv), p[2 * d + 1] - bf16_hi(hv));
-      }
+      for (int d = 0; d < 4; ++d) Ph[hg][d] = pack_f16(p[2 * d], p[2 * d + 1]);
     }
   };
   auto out_nb = [&](int nb, u32x2 v0, u32x2 v1) {
     const u32x4 vt = {v0.x, v0.y, v1.x, v1.y};
 #pragma unroll
-    for (int hg = 0; hg < HG; ++hg) {
-      O[hg][nb] = mfma16x16x32(Ph[hg], vt, O[hg][nb]);
-      O[hg][nb] = mfma16x16x32(Pl[hg], vt, O[hg][nb]);
-    }
+    for (int hg = 0; hg < HG; ++hg) O[hg][nb] = mfma16x16x32_f16(Ph[hg], vt, O[hg][nb]);
   };
   // LDS addresses as a few per-lane bases plus immediate offsets. The swizzle
   // only touches the low 3 bits of a 16-byte chunk index, so
@@ -456,8 +693,8 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
       for (int mb = 0; mb < 2; ++mb)
 #pragma unroll
         for (int hg = 0; hg < HG; ++hg) {
-          S[mb][hg] = mfma16x16x32(c[mb][0], qB[hg][2 * s], S[mb][hg]);
-          So[mb][hg] = mfma16x16x32(c[mb][1], qB[hg][2 * s + 1], So[mb][hg]);
+          S[mb][hg] = mfma16x16x32_f16(c[mb][0], qB[hg][2 * s], S[mb][hg]);
+          So[mb][hg] = mfma16x16x32_f16(c[mb][1], qB[hg][2 * s + 1], So[mb][hg]);
         }
       if (s + PFD < WPL) {
 #pragma unroll
@@ -465,11 +702,11 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
 #pragma unroll
           for (int h = 0; h < 2; ++h) nxt[k][h] = vt_read(4 * (s + PFD) + k, h);
       }
-      // issue order: (5 VALU, HG output MFMAs) x 8, the rest of the VALU,
+      // issue order: (10 VALU, HG output MFMAs) x 4, the rest of the VALU,
       // the stores, then (HG score MFMAs, 2 reads) x 4
 #pragma unroll
-      for (int k = 0; k < 8; ++k) {
-        __builtin_amdgcn_sched_group_barrier(kSchedValu, 5, 0);
+      for (int k = 0; k < 4; ++k) {
+        __builtin_amdgcn_sched_group_barrier(kSchedValu, 10, 0);
         __builtin_amdgcn_sched_group_barrier(kSchedMfma, HG, 0);
       }
       __builtin_amdgcn_sched_group_barrier(kSchedValu, 64, 0);
@@ -485,17 +722,19 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
 #pragma unroll
       for (int mb = 0; mb < 2; ++mb) S[mb][0] += S2[mb][0];
     }
+    float x[HG][8];
     if (base >= lo && base + kTile <= hi)  // an interior tile: every token is an INT2 one
-      softmax(S, [](int) { return true; }, first);
+      masked(S, [](int) { return true; }, x);
     else
-      softmax(S, [&](int tok) { return base + tok >= lo && base + tok < hi; }, first);
+      masked(S, [&](int tok) { return base + tok >= lo && base + tok < hi; }, x);
+    softmax(x, first);
   };
 
   // window tile: rows 0 .. nw-1 are positions [0, n_sink) U [rec_lo, L), the
-  // ring rows of hp_c (BF16). Wave 0 alone loads them in the score operand's
-  // layout, scores them and stores them into its buffer in the expanded
-  // layout, where the next tile's steps contract them like an INT2 tile (it is
-  // always the first unit of wave 0's pass: no output is pending before it).
+  // ring rows of hp_c (BF16, carried as fp16). Wave 0 alone loads them in the
+  // score operand's layout, scores them and stores them into its buffer in the
+  // expanded layout, where the next tile's steps contract them like an INT2
+  // tile (it is always wave 0's first unit: no output is pending before it).
   auto win_pos = [&](int i) { return i < n_sink ? i : rec_lo + (i - n_sink); };
   auto window_tile = [&](bool first) {
     f32x4 S[2][HG];
@@ -527,79 +766,55 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
       }
 #pragma unroll
       for (int j = 0; j < KL; ++j) {
-        const u32x4 v = i < nw ? pi_permute(c[mb][j]) : u32x4{0u, 0u, 0u, 0u};
+        const u32x4 v = i < nw ? bf16x8_to_f16x8(pi_permute(c[mb][j])) : u32x4{0u, 0u, 0u, 0u};
         lds_store128(wb[mb][j & 1] + 128 * (j >> 1), v);  // K-step j of row 16 mb + la
 #pragma unroll
-        for (int hg = 0; hg < HG; ++hg) S[mb][hg] = mfma16x16x32(v, qB[hg][j], S[mb][hg]);
+        for (int hg = 0; hg < HG; ++hg) S[mb][hg] = mfma16x16x32_f16(v, qB[hg][j], S[mb][hg]);
       }
     }
-    softmax(S, [&](int tok) { return tok < nw; }, first);
+    float x[HG][8];
+    masked(S, [&](int tok) { return tok < nw; }, x);
+    softmax(x, first);
   };
 
-  // ---- passes (the second only when a score outran the reference) ---------------
-  for (int pass = 0; pass < 2; ++pass) {
-    if (pass > 0) init_pass();
-    // Tile pipeline: two register slots (dn, dc) take turns, unrolled by two
-    // so that no tile is copied between them: tile i + 1's data is loaded
-    // into one slot while tile i is computed from the other, and the pages are
-    // looked up a tile before that (the first pass's first tile is already in
-    // flight from the prologue). Four independent waves per CU keep enough
-    // bytes in flight with one tile of prefetch each. The scheduling barriers
-    // keep the issue order, so the compiler's counted waits release tile i
-    // while tile i + 1's loads are in flight.
-    if (pass > 0 && n > 0) {
-      lookup(0, pgc);
-      lookup(min(1, nl), pgn);
-      __builtin_amdgcn_sched_barrier(0);
-      load(0, pgc, dn);
-      __builtin_amdgcn_sched_barrier(0);
-    }
-    bool first = pass == 0;
-    if (win_mine) {
-      window_tile(first);
-      first = false;
-    }
-    int i = 0;
-    for (; i + 1 < n; i += 2) {
-      // tile i is in dn: load tile i + 1 into dc, compute tile i
-      pgc[0] = pgn[0];
-      pgc[1] = pgn[1];
-      __builtin_amdgcn_sched_barrier(0);
-      load(i + 1, pgc, dc);
-      __builtin_amdgcn_sched_barrier(0);
-      lookup(min(i + 2, nl), pgn);
-      __builtin_amdgcn_sched_barrier(0);
-      compute(i, dn, first);
-      first = false;
-      // tile i + 1 is in dc: load tile i + 2 into dn, compute tile i + 1
-      pgc[0] = pgn[0];
-      pgc[1] = pgn[1];
-      __builtin_amdgcn_sched_barrier(0);
-      load(min(i + 2, nl), pgc, dn);
-      __builtin_amdgcn_sched_barrier(0);
-      lookup(min(i + 3, nl), pgn);
-      __builtin_amdgcn_sched_barrier(0);
-      compute(i + 1, dc, false);
-    }
-    if (i < n) {
-      compute(i, dn, first);  // the last tile (odd count), already in dn
-      first = false;
-    }
-    flush();
-    // a score above the reference by more than the slack: redo with the true maxima
-    // (the sums and accumulators of this pass are relative to m_ref, which
-    // therefore changes only when the pass is redone)
-    bool over = false;
-    float mt[HG];
-#pragma unroll
-    for (int hg = 0; hg < HG; ++hg) {
-      mt[hg] = wave_max_over_groups(m_seen[hg]);
-      over |= mt[hg] > m_ref[hg] + kRefSlack;
-    }
-    if (!__syncthreads_or(pass == 0 && over)) break;
-#pragma unroll
-    for (int hg = 0; hg < HG; ++hg) m_ref[hg] = fmaxf(m_ref[hg], mt[hg]);
+  // ---- the wave's units ------------------------------------------------------------
+  // Tile pipeline: two register slots (dn, dc) take turns, unrolled by two so
+  // that no tile is copied between them: tile i + 1's data is loaded into one
+  // slot while tile i is computed from the other, and the pages are looked up
+  // a tile before that (the first tile is already in flight from the
+  // prologue). Four independent waves per CU keep enough bytes in flight with
+  // one tile of prefetch each. The scheduling barriers keep the issue order,
+  // so the compiler's counted waits release tile i while tile i + 1's loads
+  // are in flight.
+  bool first = true;
+  if (win_mine) {
+    window_tile(true);
+    first = false;
   }
+  int i = 0;
+  for (; i + 1 < n; i += 2) {
+    // tile i is in dn: load tile i + 1 into dc, compute tile i
+    pgc[0] = pgn[0];
+    pgc[1] = pgn[1];
+    __builtin_amdgcn_sched_barrier(0);
+    load(i + 1, pgc, dc);
+    __builtin_amdgcn_sched_barrier(0);
+    lookup(min(i + 2, nl), pgn);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(i, dn, first);
+    first = false;
+    // tile i + 1 is in dc: load tile i + 2 into dn, compute tile i + 1
+    pgc[0] = pgn[0];
+    pgc[1] = pgn[1];
+    __builtin_amdgcn_sched_barrier(0);
+    load(min(i + 2, nl), pgc, dn);
+    __builtin_amdgcn_sched_barrier(0);
+    lookup(min(i + 3, nl), pgn);
+    __builtin_amdgcn_sched_barrier(0);
+    compute(i + 1, dc, false);
+  }
+  if (i < n) compute(i, dn, first);  // the last tile (odd count), already in dn
+  flush();
 
   // ---- merge the four waves: one partial per block ------------------------------
   float l_sum[HG];

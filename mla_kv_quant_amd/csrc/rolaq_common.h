@@ -28,21 +28,18 @@ __device__ __forceinline__ f32x4 mfma16x16x32(u32x4 a, u32x4 b, f32x4 c) {
                                                  __builtin_bit_cast(bf16x8_t, b), c, 0, 0, 0);
 }
 
-// D = A(16x128) * B(128x16) 2^(sb - 127) + C with A in fp4 (e2m1) and B in fp8
-// (e4m3, OCP), fp32 accumulate (v_mfma_scale_f32_16x16x128_f8f6f4, 32 cycles).
-// sb is the E8M0 block scale of the lane's 32 K-elements of B (A's scale is 1).
-// Operand layouts (checked on the device):
-//   A lane l (row l%16, G = l/16): dword d (0..3) nibble n <-> K = 64(G&1) + 16(G>>1) + 32(d>>1) + 8(d&1) + n
-//   B lane l (col l%16, G = l/16): dword i (0..7) byte b  <-> K = 32G + 4i + b
-//   C as for mfma16x16x32.
-typedef uint32_t u32x8 __attribute__((ext_vector_type(8)));
-__device__ __forceinline__ f32x4 mfma_f4_f8(u32x4 a, u32x8 b, f32x4 c, int sb) {
-  typedef int i32x4_t __attribute__((ext_vector_type(4)));
-  typedef int i32x8_t __attribute__((ext_vector_type(8)));
-  const i32x4_t a4 = __builtin_bit_cast(i32x4_t, a);
-  const i32x8_t a8 = __builtin_shufflevector(a4, a4, 0, 1, 2, 3, -1, -1, -1, -1);  // fp4 uses 4 dwords
-  return __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(a8, __builtin_bit_cast(i32x8_t, b), c, 4, 0, 0, 127, 0,
-                                                          sb);
+// The same product on fp16 inputs (same operand layout).
+typedef _Float16 f16x8_t __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ f32x4 mfma16x16x32_f16(u32x4 a, u32x4 b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8_t, a), __builtin_bit_cast(f16x8_t, b), c, 0,
+                                                0, 0);
+}
+
+// Two fp32 -> one dword of two fp16 (round to nearest even; beyond 65504 -> inf).
+__device__ __forceinline__ uint32_t pack_f16(float lo, float hi) {
+  f32x2 f = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(f, f16x2_t));
 }
 
 // Two fp32 -> one dword of two bf16 (round to nearest even), low half = lo.
@@ -76,29 +73,19 @@ __device__ __forceinline__ T gload(const void* p) {
   return *(const __attribute__((address_space(1))) T*)(p);
 }
 
-// In-place unpack of one packed word (16 codes; code p at bits 2p) into eight
-// dwords of two bf16 each. Dword k holds (code k, code k + 8) as the bf16
-// values 4 + c * 2^(e_k - 5), e = {0, 2, 4, 0, 2, 4, 0, 2}: the code bits are
-// masked straight into the mantissa of 4.0 (0x4080), so a dword costs one
-// and-or (plus a shared shift for k >= 3).
-__device__ __forceinline__ void unpack_word(uint32_t w, uint32_t d[8]) {
-  const uint32_t base = 0x40804080u;
-  d[0] = (w & 0x00030003u) | base;
-  d[1] = (w & 0x000C000Cu) | base;
-  d[2] = (w & 0x00300030u) | base;
-  const uint32_t w6 = w >> 6;
-  d[3] = (w6 & 0x00030003u) | base;
-  d[4] = (w6 & 0x000C000Cu) | base;
-  d[5] = (w6 & 0x00300030u) | base;
-  const uint32_t w12 = w >> 12;
-  d[6] = (w12 & 0x00030003u) | base;
-  d[7] = (w12 & 0x000C000Cu) | base;
+// One dword of two bf16 -> the same two values as fp16 (exact for magnitudes
+// in [2^-24, 65504] that fit fp16's 11-bit significand, which covers every bf16
+// value in [2^-17, 65504]; beyond 65504 -> inf).
+__device__ __forceinline__ uint32_t bf16x2_to_f16x2(uint32_t v) { return pack_f16(bf16_lo(v), bf16_hi(v)); }
+// One dword of two fp16 -> the same two values as bf16 (exact for fp16 values
+// that are bf16 numbers, as the decode's levels and window rows are).
+__device__ __forceinline__ uint32_t f16x2_to_bf16x2(uint32_t v) {
+  const f16x2_t h = __builtin_bit_cast(f16x2_t, v);
+  return pack_bf16((float)h[0], (float)h[1]);
 }
-
-// Mantissa shift e_k of pair k in unpack_word; the decoded value is
-// 4 + c * 2^(e_k - 5), so weights on pair k are scaled by 2^(5 - e_k).
-__host__ __device__ constexpr int pair_shift(int k) { return k < 3 ? 2 * k : (k < 6 ? 2 * k - 6 : 2 * k - 12); }
-__host__ __device__ constexpr float pair_weight(int k) { return float(1 << (5 - pair_shift(k))); }
+__device__ __forceinline__ u32x4 bf16x8_to_f16x8(u32x4 v) {
+  return u32x4{bf16x2_to_f16x2(v.x), bf16x2_to_f16x2(v.y), bf16x2_to_f16x2(v.z), bf16x2_to_f16x2(v.w)};
+}
 
 __device__ __forceinline__ float wave_max_over_groups(float v) {
   // max over lanes l, l^16, l^32, l^48 (the four 16-lane rows of a wave)

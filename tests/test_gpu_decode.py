@@ -257,10 +257,11 @@ def test_request_without_ring_rows_and_reused_index():
 
 
 @pytest.mark.parametrize("win", [(4, 16), (0, 0)], ids=["P4W16", "P0W0"])
-def test_redo_when_scores_outgrow_the_first_tile(win):
-    """Logits with std 60 (log2 units ~87): later tiles' scores exceed every
-    wave's first-tile reference by more than the 2^64 headroom, so the block
-    redoes its tiles against the true maxima (restaging the window rows)."""
+def test_rescale_when_scores_outgrow_the_reference(win):
+    """Logits with std 60 (log2 units ~87): later tiles' maxima exceed each
+    wave's reference (its first tile's maximum) by far more than the 2^15 that
+    an fp16 probability can hold, so the waves move their references and scale
+    their accumulated sums and outputs many times over, in place."""
     D, R, H = 512, 64, 16
     P, W = win
     lengths = [2000, 1300]

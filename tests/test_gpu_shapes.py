@@ -132,7 +132,9 @@ def test_cfg3_ragged_paged_split_vs_unsplit():
     splits = [math.ceil(v / 2048) for v in lengths]
     out, lse = _decode(gp, q, slots, pages, lengths, reqs, page, splits, 4, P, W, sm)
     one, _ = _decode(gp, q, slots, pages, lengths, reqs, page, [1] * B, 4, P, W, sm)
-    torch.testing.assert_close(out, one, rtol=2 ** -7, atol=1e-3)
+    # the two runs round their fp16 probabilities against different references
+    # (relative 2^-12 each), so they agree to the attention bar, not bit for bit
+    torch.testing.assert_close(out, one, rtol=RTOL, atol=ATOL)
     _check_sampled(gpu_pool_to_oracle(gp), q, out, lse, slots, lengths, reqs, splits, P, W, sm, D,
                    [0, 17, 64, 127])
 
