@@ -167,31 +167,6 @@ class DecodeBench:
     def flops_per_layer(self) -> float:
         return float(2 * int(self.lengths.sum()) * self.H * (2 * self.D + self.R))
 
-    def splits_for(self, policy):
-        """num_kv_splits per request: an int for all, or ("len", T): one INT2
-        split per T tokens of the request plus the window split (a caller's
-        per-request choice, as SGLang sizes splits by sequence length)."""
-        if isinstance(policy, int):
-            return torch.full((self.B,), policy, dtype=torch.int32, device=self.dev), policy
-        per = np.maximum(1, np.ceil(self.lengths / policy[1]).astype(np.int64)) + 1
-        return torch.from_numpy(per.astype(np.int32)).to(self.dev), int(per.max())
-
-    def pick_splits(self, candidates, layers_label: str = ""):
-        best = None
-        for pol in candidates:
-            ns, mx = self.splits_for(pol)
-            self.alloc_scratch(mx)
-            self.ns = ns
-            ms = time_loop(self.step, 2, 1)
-            print(f"[bench] {layers_label}splits={pol}: {ms * 1000 / self.layers:.2f} us/layer", file=sys.stderr,
-                  flush=True)
-            if best is None or ms < best[1]:
-                best = (pol, ms)
-        ns, mx = self.splits_for(best[0])
-        self.alloc_scratch(mx)
-        self.ns = ns
-        return best[0] if isinstance(best[0], int) else f"len/{best[0][1]}"
-
 
 def time_loop(fn, steps: int, warmup: int) -> float:
     """Milliseconds per step: events on the current stream around exactly ``steps`` steps."""
@@ -331,7 +306,8 @@ class ExtendBench:
             self.layers.append(c)
         self.out = torch.empty(B * TQ, H, D, dtype=torch.bfloat16, device=dev)
         # key rows gathered per call (one layer at a time: one workspace serves all layers)
-        self.ws = torch.empty(B * (PF + TQ), D + R, dtype=torch.bfloat16, device=dev)
+        self.key_rows = B * (PF + TQ)
+        self.ws = torch.empty(self.key_rows, D + R, dtype=torch.float16, device=dev)
         torch.cuda.synchronize()
 
     def step(self):
@@ -340,7 +316,7 @@ class ExtendBench:
         for c in self.layers:
             kernels.extend_fwd(c["q"], c["kc"], self.qo_indptr, self.kv_indptr, self.kv_indices, self.prefix,
                                self.req, c["codes"], c["params"], c["rope"], c["hp"], self.TQ, self.out,
-                               self.sm_scale, self.P, self.W, self.PAGE, workspace=self.ws)
+                               self.sm_scale, self.P, self.W, self.PAGE, workspace=self.ws, key_rows=self.key_rows)
 
     def flops_per_layer(self) -> float:
         """Algorithmic flops: 2 H (2 D + R) per (query, visible key) pair."""
@@ -490,21 +466,39 @@ def copy_probe(nbytes: int = 1 << 30, reps: int = 10) -> float:
 
 
 def reported_decode_result(args, dev: str, name: str) -> dict:
-    """cfg3 (ragged large batch) or cfg4a (MiniCPM3 shape) decode, 4 layers with their own buffers."""
+    """Decode at the library's own split policy (the reference's 129 splits requested,
+    capped by the library at one working block per CU): cfg3 (ragged large batch) and
+    cfg4a (MiniCPM3 shape), 4 layers with their own buffers; "serve_b8" / "serve_b16":
+    DeepSeek-V2-Lite shape at the reference's serving batch sizes (serve.py:157-158,164),
+    8 layers."""
+    from mla_kv_quant_amd import kernels
+
     layers = 4
     if name == "cfg3":
         lens = np.random.default_rng(3).integers(2048, 8193, size=128)
         db = DecodeBench(layers, dev, B=128, lengths=lens, H=16, D=512, R=64, seed=3)
         workload = "cfg3 decode: batch 128, ragged context U[2048,8192], 16 heads, latent 512, rope 64, page 64 shuffled"
-        cands = [2, 3, 4, 5, 6, 8, ("len", 768), ("len", 1024), ("len", 1536), ("len", 2048)]
-    else:
+    elif name == "cfg4a":
         db = DecodeBench(layers, dev, B=64, lengths=[16384] * 64, H=40, D=256, R=32, seed=4)
         workload = "cfg4a decode: batch 64 x context 16384, 40 heads, latent 256, rope 32, page 64 shuffled"
-        cands = [4, 5, 6, 8, 9]
-    ns = db.pick_splits(cands, f"{name} ")
-    ms = time_loop(db.step, max(5, args.steps // 2), args.warmup)
+    else:
+        B = int(name[len("serve_b"):])
+        layers = 8
+        db = DecodeBench(layers, dev, B=B, seed=5 + B)
+        workload = (f"serving decode: batch {B} x context 16384, 16 heads, latent 512, rope 64, page 64 shuffled "
+                    f"(the reference's graph batch sizes, serve.py:157-158,164)")
+    db.alloc_scratch(129)
+    db.set_splits(129)  # the reference's static split count (serve.py:121,163,198)
+    ns = kernels.decode_split_cap(db.B, db.H, db.D, 129)
+    steps = max(5, args.steps // 2)
+    time_loop(db.step, steps, args.warmup)  # a first pass over fresh buffers runs slower: not timed
+    ms = float(np.median([time_loop(db.step, steps, 1) for _ in range(3)]))
     us = ms * 1000.0 / layers
-    ms1 = time_loop(db.step_partials, max(5, args.steps // 2), args.warmup)
+    # stage 1 alone (decode_partials honours the count and launches max_kv_splits + 1
+    # split rows) at the count the fused call used, with scratch sized to it
+    db.alloc_scratch(ns)
+    db.set_splits(ns)
+    ms1 = float(np.median([time_loop(db.step_partials, steps, 1) for _ in range(3)]))
     us1 = ms1 * 1000.0 / layers
     ach1 = db.bytes_per_layer(with_out=False) / (us1 * 1e-6) / 1e9
     res = {
@@ -515,7 +509,8 @@ def reported_decode_result(args, dev: str, name: str) -> dict:
         "stage1_gbs": round(ach1, 1),
         "stage1_hbm_frac": round(ach1 / HBM_PEAK_GBS, 4),
         "mfma_frac": round(db.flops_per_layer() / (us1 * 1e-6) / 1e12 / MFMA_BF16_PEAK_TFLOPS, 4),
-        "num_kv_splits": ns,
+        "num_kv_splits_requested": 129,
+        "num_kv_splits_used": ns,
         "tokens": int(db.lengths.sum()),
     }
     print(f"[bench] {name}: {us:.2f} us/layer, stage 1 {us1:.2f} us ({ach1:.0f} GB/s)", file=sys.stderr, flush=True)
@@ -605,7 +600,7 @@ def main():
         print(json.dumps(extend_result(args, dev)), flush=True)
         return
     if args.reported_only:
-        out = {k: reported_decode_result(args, dev, k) for k in ("cfg3", "cfg4a")}
+        out = {k: reported_decode_result(args, dev, k) for k in ("cfg3", "cfg4a", "serve_b8", "serve_b16")}
         out["qdq"] = qdq_result(args, dev)
         print(json.dumps(out), flush=True)
         return
@@ -649,12 +644,12 @@ def main():
         "higher_is_better": False,
         "scaling": "weak",
         "vs_baseline": None,
-        "dtype": "int2-cache/bf16-mfma/fp32-acc",
+        "dtype": "int2-cache/fp16-mfma(latent)+bf16-mfma(rope)/fp32-acc",
         "data": "synthetic (seeded N(0,1) latents, 1% outlier channels x20, seeded orthogonal rotations)",
         "config": {"workload": "cfg2 decode: batch 32 x context 16384, 16 heads, latent 512, rope 64, "
                                "s4r16 window, page 64 shuffled, 27 layers with own buffers",
                    "batch": db.B, "context": db.L, "heads": db.H, "layers": args.layers,
-                   "num_kv_splits": ns_best, "split_policy": "ceil(CUs / B) + 1",
+                   "num_kv_splits": ns_best, "split_policy": "ceil(CUs / B) + 1 (the library's cap)",
                    "us_per_layer_at_129_splits": round(ms129 * 1000.0 / args.layers, 3)},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": read_traffic(),
@@ -675,7 +670,8 @@ def main():
     if not args.no_extend:
         result["extend"] = extend_result(args, dev)
     if not args.no_reported:
-        result["reported"] = {k: reported_decode_result(args, dev, k) for k in ("cfg3", "cfg4a")}
+        result["reported"] = {k: reported_decode_result(args, dev, k)
+                              for k in ("cfg3", "cfg4a", "serve_b8", "serve_b16")}
         result["reported"]["qdq"] = qdq_result(args, dev)
     if not args.no_cpu:
         if not hasattr(db, "caches"):

@@ -134,15 +134,21 @@ int rolaq_prepare_gf_splits(const int32_t* splits, int32_t* quant, int32_t* merg
  * positions are written in order (SGLang serves RoLaQ with its radix cache
  * disabled, deployment/serve.py:149).
  * num_kv_splits: int32 [B] requested splits ns_b (1 <= ns_b <= max_kv_splits);
- * positions P <= t < L_b - W and the window rows are split over
- * max(ns_b - 1, 1) splits (the window rows go with split 0); split
- * max(ns_b - 1, 1), the reference's window split, holds the neutral partial.
+ * request b uses ns'_b = min(ns_b, cap) splits, cap as rolaq_decode_split_cap
+ * returns it (about one working block per compute unit: more splits only
+ * add partials to write and merge, and SGLang reads only the merged output;
+ * the output does not depend on the split count beyond FP32 summation order).
+ * Positions P <= t < L_b - W and the window rows are split over
+ * max(ns'_b - 1, 1) splits (the window rows go with split 0); split
+ * max(ns'_b - 1, 1), the reference's window split, holds the neutral partial.
  * Partials (normalised output, natural-log LSE; empty splits 0 / -1e4) go to
  * attn_logits fp32 [B, H, max_kv_splits + 1, D] (16-byte aligned) and
  * attn_lse fp32 [B, H, max_kv_splits + 1]; the merged output to out: bf16
  * [B, H, D] with strides (out_stride_b, out_stride_h), in the rotated frame.
  * Supported shapes: (D, R) = (512, 64) or (256, 32), 1 <= H <= 128; window
- * P + W <= 32.
+ * P + W <= 32. Latent values (query, stored levels, window rows) are carried
+ * in fp16 on the way to the MFMAs: magnitudes above 65504 make that
+ * request's output non-finite.
  */
 int rolaq_decode_fwd(const void* q, int64_t q_stride_b, int64_t q_stride_h, const uint8_t* codes,
                      const float* params, const void* rope_buf, const void* hp_c,
@@ -175,8 +181,18 @@ int rolaq_decode_fwd_noalloc(const void* q, int64_t q_stride_b, int64_t q_stride
                              int64_t out_stride_h, void* stream);
 
 /*
+ * The split cap of rolaq_decode_fwd and rolaq_decode_fwd_noalloc on the
+ * current device: ceil(CUs / (B * head blocks)) + 1, at most max_kv_splits
+ * (a head block is 16 heads at D = 512 and up to 48 at D = 256), written to
+ * *cap. Host only: no launch, no synchronisation. No counterpart in the
+ * reference, whose stage 1 runs every requested split.
+ */
+int rolaq_decode_split_cap(int B, int H, int D, int max_kv_splits, int* cap);
+
+/*
  * Stage 1 of rolaq_decode_fwd alone: the split partials and their LSE, with
- * the same arguments and rules (no output). Replaces the quantized stage-1
+ * the same arguments and rules (no output), every request at its requested
+ * split count ns_b (no cap). Replaces the quantized stage-1
  * grid plus _fwd_hp_window_stage1 of packed_mla_decode_gf_fwd
  * (deployment/patches/rolaq_sglang.patch:94-111), for callers that merge
  * themselves or time the stages apart.
@@ -217,21 +233,24 @@ int rolaq_decode_merge(const float* attn_logits, const float* attn_lse, const in
  * out: bf16 [T, H, D], strides (out_stride_t, out_stride_h), rotated frame.
  * max_q_len >= every chunk length (sizes the grid). (D, R) = (256, 32) or
  * (512, 64).
- * workspace: caller-owned bf16 [workspace_rows, D + R], 16-byte aligned; the
- * call first gathers every key row of the extended sequences into it
- * (sequence b at rows koff_b .., koff_b = sum over b' < b of
- * prefix_lens[b'] + chunk length b'), so workspace_rows must be at least
- * sum_b (prefix_lens[b] + chunk length b). Rows past workspace_rows are never
- * written (their keys then read as zeros: a short workspace gives wrong
- * outputs, never an out-of-bounds access). Its contents are scratch.
+ * workspace: caller-owned scratch of 16-bit elements [workspace_rows, D + R],
+ * 16-byte aligned; the call first gathers every key row of the extended
+ * sequences into it as fp16 (sequence b at rows koff_b .., koff_b = sum over
+ * b' < b of prefix_lens[b'] + chunk length b'). key_rows is that sum over all
+ * b, sum_b (prefix_lens[b] + chunk length b), as the caller knows it on the
+ * host (SGLang: extend_prefix_lens_cpu and the token count): a workspace
+ * shorter than key_rows is rejected (ROLAQ_ERR_INVALID, nothing launched).
+ * Rows past workspace_rows are never written; a sequence whose rows do not
+ * fit (key_rows short of the device-side sum) gets NaN outputs.
+ * Latent values are carried in fp16 as for rolaq_decode_fwd.
  */
 int rolaq_extend_fwd(const void* q, int64_t q_stride_t, int64_t q_stride_h, const void* k_chunk,
                      int64_t kc_stride_t, const int32_t* qo_indptr, const int32_t* kv_indptr,
                      const int32_t* kv_indices, int page_size, const int64_t* prefix_lens,
                      const int64_t* req_idx, int max_reqs, const uint8_t* codes, const float* params,
                      const void* rope_buf, const void* hp_c, int B, int H, int D, int R, int P, int W,
-                     int max_q_len, float sm_scale, void* workspace, int64_t workspace_rows, void* out,
-                     int64_t out_stride_t, int64_t out_stride_h, void* stream);
+                     int max_q_len, float sm_scale, void* workspace, int64_t workspace_rows, int64_t key_rows,
+                     void* out, int64_t out_stride_t, int64_t out_stride_h, void* stream);
 
 /*
  * Cache rows as bf16 [latent | rope] rows (MHA-style prefill over a packed

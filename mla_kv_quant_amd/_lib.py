@@ -40,12 +40,13 @@ SIGNATURES = {
     "rolaq_decode_partials": [c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                               c_void_p, c_int, c_void_p, c_void_p, c_int, c_void_p, c_int, c_int, c_int, c_int,
                               c_int, c_int, c_int, c_float, c_void_p, c_void_p, c_void_p],
+    "rolaq_decode_split_cap": [c_int, c_int, c_int, c_int, c_void_p],
     "rolaq_decode_merge": [c_void_p, c_void_p, c_void_p, c_int, c_int, c_int, c_int, c_void_p, c_int64,
                            c_int64, c_void_p],
     "rolaq_extend_fwd": [c_void_p, c_int64, c_int64, c_void_p, c_int64, c_void_p, c_void_p, c_void_p, c_int,
                          c_void_p, c_void_p, c_int, c_void_p, c_void_p, c_void_p, c_void_p, c_int, c_int, c_int,
-                         c_int, c_int, c_int, c_int, c_float, c_void_p, c_int64, c_void_p, c_int64, c_int64,
-                         c_void_p],
+                         c_int, c_int, c_int, c_int, c_float, c_void_p, c_int64, c_int64, c_void_p, c_int64,
+                         c_int64, c_void_p],
     "rolaq_assemble_rows": [c_void_p, c_int64, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p, c_void_p,
                             c_void_p, c_int, c_int, c_void_p, c_int64, c_void_p],
 }

@@ -64,7 +64,7 @@ extern "C" {
 
 const char* rolaq_last_error(void) { return g_err; }
 
-int rolaq_abi_version(void) { return 3; }
+int rolaq_abi_version(void) { return 4; }
 
 int rolaq_scatter_pack_rows(const float* x, int64_t x_stride, const int32_t* slots, int64_t n, int D,
                             int group_size, float threshold, double gain, uint8_t* codes, float* params,
@@ -254,6 +254,7 @@ int decode_args(const char* who, const void* q, int64_t q_stride_b, int64_t q_st
   a->seq_lens = seq_lens;
   a->req_idx = req_idx;
   a->num_kv_splits = num_kv_splits;
+  a->split_cap = max_kv_splits;
   a->S1 = max_kv_splits + 1;
   a->max_reqs = max_reqs;
   a->B = B;
@@ -266,9 +267,30 @@ int decode_args(const char* who, const void* q, int64_t q_stride_b, int64_t q_st
   return ROLAQ_OK;
 }
 
+// The split count the fused decode uses at most: enough quantized splits for
+// one working block per compute unit over the batch's (sequence, head block)
+// pairs, plus the window split, and never more than the caller's maximum.
+// Every request then takes min(its num_kv_splits, this); the merged output
+// does not depend on the split count (up to FP32 summation order).
+int fused_split_cap(int B, int H, int D, int max_kv_splits) {
+  const int64_t units = int64_t(B) * rolaq_decode_head_blocks(D, H);
+  const int64_t quant = (cu_count() + units - 1) / units;
+  const int64_t cap = (quant < 1 ? 1 : quant) + 1;
+  return cap < max_kv_splits ? int(cap) : max_kv_splits;
+}
+
 }  // namespace
 
 extern "C" {
+
+int rolaq_decode_split_cap(int B, int H, int D, int max_kv_splits, int* cap) {
+  if (B < 1 || H <= 0 || H > kMaxHeads || (D != 512 && D != 256) || max_kv_splits < 1 || max_kv_splits > 4096 ||
+      !cap)
+    return fail(ROLAQ_ERR_INVALID, "decode_split_cap: invalid B, H, D, max_kv_splits or null cap");
+  *cap = fused_split_cap(B, H, D, max_kv_splits);
+  g_err[0] = '\0';
+  return ROLAQ_OK;
+}
 
 int rolaq_decode_fwd(const void* q, int64_t q_stride_b, int64_t q_stride_h, const uint8_t* codes,
                      const float* params, const void* rope_buf, const void* hp_c, const int32_t* kv_indptr,
@@ -285,6 +307,7 @@ int rolaq_decode_fwd(const void* q, int64_t q_stride_b, int64_t q_stride_h, cons
                              D, R, P, W, sm_scale, attn_logits, attn_lse, &a);
   if (rc != ROLAQ_OK) return rc;
   if (!out) return fail(ROLAQ_ERR_INVALID, "decode_fwd: null pointer");
+  a.split_cap = fused_split_cap(B, H, D, max_kv_splits);
   return hip_status(rolaq_launch_decode(a, D, R, max_kv_splits, static_cast<uint16_t*>(out), out_stride_b,
                                         out_stride_h, kStagePartials | kStageMerge, static_cast<hipStream_t>(stream)),
                     "decode_fwd launch");
@@ -320,6 +343,7 @@ int rolaq_decode_fwd_noalloc(const void* q, int64_t q_stride_b, int64_t q_stride
                              max_kv_splits, B, H, D, R, P, W, sm_scale, logits, lse, &a);
   if (rc != ROLAQ_OK) return rc;
   if (!out) return fail(ROLAQ_ERR_INVALID, "decode_fwd_noalloc: null pointer");
+  a.split_cap = fused_split_cap(B, H, D, max_kv_splits);
   return hip_status(rolaq_launch_decode(a, D, R, max_kv_splits, static_cast<uint16_t*>(out), out_stride_b,
                                         out_stride_h, kStagePartials | kStageMerge, static_cast<hipStream_t>(stream)),
                     "decode_fwd_noalloc launch");
@@ -355,6 +379,7 @@ int rolaq_decode_merge(const float* attn_logits, const float* attn_lse, const in
   if (!aligned(attn_logits, 16)) return fail(ROLAQ_ERR_INVALID, "decode_merge: attn_logits must be 16-byte aligned");
   rolaq::DecodeArgs a{};
   a.num_kv_splits = num_kv_splits;
+  a.split_cap = max_kv_splits;
   a.S1 = max_kv_splits + 1;
   a.B = B;
   a.H = H;
@@ -370,8 +395,8 @@ int rolaq_extend_fwd(const void* q, int64_t q_stride_t, int64_t q_stride_h, cons
                      const int32_t* kv_indices, int page_size, const int64_t* prefix_lens,
                      const int64_t* req_idx, int max_reqs, const uint8_t* codes, const float* params,
                      const void* rope_buf, const void* hp_c, int B, int H, int D, int R, int P, int W, int max_q_len,
-                     float sm_scale, void* workspace, int64_t workspace_rows, void* out, int64_t out_stride_t,
-                     int64_t out_stride_h, void* stream) {
+                     float sm_scale, void* workspace, int64_t workspace_rows, int64_t key_rows, void* out,
+                     int64_t out_stride_t, int64_t out_stride_h, void* stream) {
   if (B < 0 || max_q_len < 0) return fail(ROLAQ_ERR_INVALID, "extend_fwd: B < 0 or max_q_len < 0");
   if (B == 0 || max_q_len == 0) { g_err[0] = '\0'; return ROLAQ_OK; }
   if (!((D == 256 && R == 32) || (D == 512 && R == 64)))
@@ -382,6 +407,11 @@ int rolaq_extend_fwd(const void* q, int64_t q_stride_t, int64_t q_stride_h, cons
     return fail(ROLAQ_ERR_INVALID, "extend_fwd: null pointer");
   if (workspace_rows < 1 || !aligned(workspace, 16))
     return fail(ROLAQ_ERR_INVALID, "extend_fwd: workspace must be 16-byte aligned with at least one row");
+  if (key_rows < 0 || workspace_rows < key_rows)
+    return fail(ROLAQ_ERR_INVALID,
+                "extend_fwd: workspace of %lld rows is short of the %lld key rows (sum of prefix_lens and chunk "
+                "lengths) it must hold",
+                (long long)workspace_rows, (long long)key_rows);
   if (page_size < 1 || (page_size & (page_size - 1)))
     return fail(ROLAQ_ERR_INVALID, "extend_fwd: page_size must be a power of two, got %d", page_size);
   if (P < 0 || W < 0) return fail(ROLAQ_ERR_INVALID, "extend_fwd: negative window");

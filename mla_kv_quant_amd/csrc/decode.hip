@@ -136,202 +136,6 @@ __device__ __forceinline__ void expand_word(uint32_t w, const Lut& t, u32x4& c0,
   }
 }
 
-// In-place scaling of an output accumulator held in an AGPR tuple. The
-// compiler prints an "a" operand of four floats as a[b:b+3]; the assembler
-// macro ROLAQ_ACC_BASE recovers b by comparing that text with every even base
-// (an operand anywhere else stops the assembly with an error), so that
-// ROLAQ_ACC_SCALE can read, scale and write the four registers one by one
-// (v_accvgpr_read / v_mul_f32 / v_accvgpr_write) without the compiler ever
-// seeing the accumulators leave their registers. Inline asm blobs share one
-// assembler state in order of emission, so the definitions are made once, at
-// the start of each kernel.
-#define ROLAQ_ACC_CASE(k, k3) "  .ifc \\t, a[" #k ":" #k3 "]\n    .set rolaq_acc_b, " #k "\n  .endif\n"
-#define ROLAQ_ACC_CASES \
-  ROLAQ_ACC_CASE(0, 3) \
-  ROLAQ_ACC_CASE(2, 5) \
-  ROLAQ_ACC_CASE(4, 7) \
-  ROLAQ_ACC_CASE(6, 9) \
-  ROLAQ_ACC_CASE(8, 11) \
-  ROLAQ_ACC_CASE(10, 13) \
-  ROLAQ_ACC_CASE(12, 15) \
-  ROLAQ_ACC_CASE(14, 17) \
-  ROLAQ_ACC_CASE(16, 19) \
-  ROLAQ_ACC_CASE(18, 21) \
-  ROLAQ_ACC_CASE(20, 23) \
-  ROLAQ_ACC_CASE(22, 25) \
-  ROLAQ_ACC_CASE(24, 27) \
-  ROLAQ_ACC_CASE(26, 29) \
-  ROLAQ_ACC_CASE(28, 31) \
-  ROLAQ_ACC_CASE(30, 33) \
-  ROLAQ_ACC_CASE(32, 35) \
-  ROLAQ_ACC_CASE(34, 37) \
-  ROLAQ_ACC_CASE(36, 39) \
-  ROLAQ_ACC_CASE(38, 41) \
-  ROLAQ_ACC_CASE(40, 43) \
-  ROLAQ_ACC_CASE(42, 45) \
-  ROLAQ_ACC_CASE(44, 47) \
-  ROLAQ_ACC_CASE(46, 49) \
-  ROLAQ_ACC_CASE(48, 51) \
-  ROLAQ_ACC_CASE(50, 53) \
-  ROLAQ_ACC_CASE(52, 55) \
-  ROLAQ_ACC_CASE(54, 57) \
-  ROLAQ_ACC_CASE(56, 59) \
-  ROLAQ_ACC_CASE(58, 61) \
-  ROLAQ_ACC_CASE(60, 63) \
-  ROLAQ_ACC_CASE(62, 65) \
-  ROLAQ_ACC_CASE(64, 67) \
-  ROLAQ_ACC_CASE(66, 69) \
-  ROLAQ_ACC_CASE(68, 71) \
-  ROLAQ_ACC_CASE(70, 73) \
-  ROLAQ_ACC_CASE(72, 75) \
-  ROLAQ_ACC_CASE(74, 77) \
-  ROLAQ_ACC_CASE(76, 79) \
-  ROLAQ_ACC_CASE(78, 81) \
-  ROLAQ_ACC_CASE(80, 83) \
-  ROLAQ_ACC_CASE(82, 85) \
-  ROLAQ_ACC_CASE(84, 87) \
-  ROLAQ_ACC_CASE(86, 89) \
-  ROLAQ_ACC_CASE(88, 91) \
-  ROLAQ_ACC_CASE(90, 93) \
-  ROLAQ_ACC_CASE(92, 95) \
-  ROLAQ_ACC_CASE(94, 97) \
-  ROLAQ_ACC_CASE(96, 99) \
-  ROLAQ_ACC_CASE(98, 101) \
-  ROLAQ_ACC_CASE(100, 103) \
-  ROLAQ_ACC_CASE(102, 105) \
-  ROLAQ_ACC_CASE(104, 107) \
-  ROLAQ_ACC_CASE(106, 109) \
-  ROLAQ_ACC_CASE(108, 111) \
-  ROLAQ_ACC_CASE(110, 113) \
-  ROLAQ_ACC_CASE(112, 115) \
-  ROLAQ_ACC_CASE(114, 117) \
-  ROLAQ_ACC_CASE(116, 119) \
-  ROLAQ_ACC_CASE(118, 121) \
-  ROLAQ_ACC_CASE(120, 123) \
-  ROLAQ_ACC_CASE(122, 125) \
-  ROLAQ_ACC_CASE(124, 127) \
-  ROLAQ_ACC_CASE(126, 129) \
-  ROLAQ_ACC_CASE(128, 131) \
-  ROLAQ_ACC_CASE(130, 133) \
-  ROLAQ_ACC_CASE(132, 135) \
-  ROLAQ_ACC_CASE(134, 137) \
-  ROLAQ_ACC_CASE(136, 139) \
-  ROLAQ_ACC_CASE(138, 141) \
-  ROLAQ_ACC_CASE(140, 143) \
-  ROLAQ_ACC_CASE(142, 145) \
-  ROLAQ_ACC_CASE(144, 147) \
-  ROLAQ_ACC_CASE(146, 149) \
-  ROLAQ_ACC_CASE(148, 151) \
-  ROLAQ_ACC_CASE(150, 153) \
-  ROLAQ_ACC_CASE(152, 155) \
-  ROLAQ_ACC_CASE(154, 157) \
-  ROLAQ_ACC_CASE(156, 159) \
-  ROLAQ_ACC_CASE(158, 161) \
-  ROLAQ_ACC_CASE(160, 163) \
-  ROLAQ_ACC_CASE(162, 165) \
-  ROLAQ_ACC_CASE(164, 167) \
-  ROLAQ_ACC_CASE(166, 169) \
-  ROLAQ_ACC_CASE(168, 171) \
-  ROLAQ_ACC_CASE(170, 173) \
-  ROLAQ_ACC_CASE(172, 175) \
-  ROLAQ_ACC_CASE(174, 177) \
-  ROLAQ_ACC_CASE(176, 179) \
-  ROLAQ_ACC_CASE(178, 181) \
-  ROLAQ_ACC_CASE(180, 183) \
-  ROLAQ_ACC_CASE(182, 185) \
-  ROLAQ_ACC_CASE(184, 187) \
-  ROLAQ_ACC_CASE(186, 189) \
-  ROLAQ_ACC_CASE(188, 191) \
-  ROLAQ_ACC_CASE(190, 193) \
-  ROLAQ_ACC_CASE(192, 195) \
-  ROLAQ_ACC_CASE(194, 197) \
-  ROLAQ_ACC_CASE(196, 199) \
-  ROLAQ_ACC_CASE(198, 201) \
-  ROLAQ_ACC_CASE(200, 203) \
-  ROLAQ_ACC_CASE(202, 205) \
-  ROLAQ_ACC_CASE(204, 207) \
-  ROLAQ_ACC_CASE(206, 209) \
-  ROLAQ_ACC_CASE(208, 211) \
-  ROLAQ_ACC_CASE(210, 213) \
-  ROLAQ_ACC_CASE(212, 215) \
-  ROLAQ_ACC_CASE(214, 217) \
-  ROLAQ_ACC_CASE(216, 219) \
-  ROLAQ_ACC_CASE(218, 221) \
-  ROLAQ_ACC_CASE(220, 223) \
-  ROLAQ_ACC_CASE(222, 225) \
-  ROLAQ_ACC_CASE(224, 227) \
-  ROLAQ_ACC_CASE(226, 229) \
-  ROLAQ_ACC_CASE(228, 231) \
-  ROLAQ_ACC_CASE(230, 233) \
-  ROLAQ_ACC_CASE(232, 235) \
-  ROLAQ_ACC_CASE(234, 237) \
-  ROLAQ_ACC_CASE(236, 239) \
-  ROLAQ_ACC_CASE(238, 241) \
-  ROLAQ_ACC_CASE(240, 243) \
-  ROLAQ_ACC_CASE(242, 245) \
-  ROLAQ_ACC_CASE(244, 247) \
-  ROLAQ_ACC_CASE(246, 249) \
-  ROLAQ_ACC_CASE(248, 251) \
-  ROLAQ_ACC_CASE(250, 253) \
-  ROLAQ_ACC_CASE(252, 255)
-// Defines the macros for the rest of the assembly (each kernel calls it first;
-// the assembler keeps the definitions, and the guard skips a second one).
-__device__ __forceinline__ void define_acc_macros() {
-  asm volatile(
-    ".ifndef rolaq_acc_macros\n"
-    ".set rolaq_acc_macros, 1\n"
-    ".macro ROLAQ_ACC_BASE t\n"
-    "  .set rolaq_acc_b, -1\n" ROLAQ_ACC_CASES
-    "  .if rolaq_acc_b < 0\n"
-    "    .error \"ROLAQ_ACC_BASE: not an AGPR tuple\"\n"
-    "  .endif\n"
-    ".endm\n"
-    ".macro ROLAQ_ACC_SCALE t, t0, t1, t2, t3, f0, f1, f2, f3\n"
-    "  ROLAQ_ACC_BASE \\t\n"
-    "  v_accvgpr_read_b32 \\t0, a[rolaq_acc_b]\n"
-    "  v_accvgpr_read_b32 \\t1, a[rolaq_acc_b+1]\n"
-    "  v_accvgpr_read_b32 \\t2, a[rolaq_acc_b+2]\n"
-    "  v_accvgpr_read_b32 \\t3, a[rolaq_acc_b+3]\n"
-    "  s_nop 1\n"
-    "  v_mul_f32_e32 \\t0, \\t0, \\f0\n"
-    "  v_mul_f32_e32 \\t1, \\t1, \\f1\n"
-    "  v_mul_f32_e32 \\t2, \\t2, \\f2\n"
-    "  v_mul_f32_e32 \\t3, \\t3, \\f3\n"
-    "  s_nop 1\n"
-    "  v_accvgpr_write_b32 a[rolaq_acc_b], \\t0\n"
-    "  v_accvgpr_write_b32 a[rolaq_acc_b+1], \\t1\n"
-    "  v_accvgpr_write_b32 a[rolaq_acc_b+2], \\t2\n"
-    "  v_accvgpr_write_b32 a[rolaq_acc_b+3], \\t3\n"
-    ".endm\n"
-    ".endif\n");
-}
-#undef ROLAQ_ACC_CASES
-#undef ROLAQ_ACC_CASE
-
-// Four output accumulators, element j of each scaled by f_j in place when
-// need (a lane mask) is not 0. The branch is inside the asm: for the compiler
-// the accumulators flow through unchanged in their registers, so the rare
-// rescale adds no copies at a join. The leading waits cover the output MFMA
-// that last wrote them (tens of instructions earlier), the trailing ones an
-// MFMA that reads them next.
-__device__ __forceinline__ void scale_acc4(f32x4& a, f32x4& b, f32x4& c, f32x4& d, const float (&f)[4],
-                                           uint64_t need) {
-  float t0, t1, t2, t3;
-  asm volatile(
-      "s_cmp_lg_u64 %12, 0\n\t"
-      "s_cbranch_scc0 1f\n\t"
-      "s_nop 7\n\ts_nop 7\n\t"
-      "ROLAQ_ACC_SCALE %0, %4, %5, %6, %7, %8, %9, %10, %11\n\t"
-      "ROLAQ_ACC_SCALE %1, %4, %5, %6, %7, %8, %9, %10, %11\n\t"
-      "ROLAQ_ACC_SCALE %2, %4, %5, %6, %7, %8, %9, %10, %11\n\t"
-      "ROLAQ_ACC_SCALE %3, %4, %5, %6, %7, %8, %9, %10, %11\n\t"
-      "s_nop 7\n"
-      "1:"
-      : "+a"(a), "+a"(b), "+a"(c), "+a"(d), "=&v"(t0), "=&v"(t1), "=&v"(t2), "=&v"(t3)
-      : "v"(f[0]), "v"(f[1]), "v"(f[2]), "v"(f[3]), "s"(need)
-      : "scc");
-}
-
 __device__ __forceinline__ void lds_store128(uint8_t* p, u32x4 v) { *reinterpret_cast<u32x4*>(p) = v; }
 __device__ __forceinline__ u32x4 lds_load128(const uint8_t* p) { return *reinterpret_cast<const u32x4*>(p); }
 
@@ -412,7 +216,7 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
 #pragma unroll
     for (int kr = 0; kr < KR; ++kr) qR[hg][kr] = gload<u32x4>(qh + D + 32 * kr + 8 * gq);
   }
-  const int ns = a.num_kv_splits[b];
+  const int ns = min(a.num_kv_splits[b], a.split_cap);
   const int kv0 = a.kv_indptr[b], kv1 = a.kv_indptr[b + 1];
   const int64_t req = a.req_idx[b];
   const int64_t slv = (a.seq_lens ? a.seq_lens : a.req_idx)[b];  // no branch before the loads
@@ -889,11 +693,11 @@ template <int D>
 __global__ __launch_bounds__(128) void decode_stage2(const float* __restrict__ logits,
                                                      const float* __restrict__ lse,
                                                      const int32_t* __restrict__ num_kv_splits,
-                                                     int H, int S1, uint16_t* out, int64_t o_sb,
-                                                     int64_t o_sh) {
+                                                     int split_cap, int H, int S1, uint16_t* out,
+                                                     int64_t o_sb, int64_t o_sh) {
   constexpr int FPT = D / 128;
   const int b = blockIdx.x / H, h = blockIdx.x % H;
-  const int nq = min(max(num_kv_splits[b] - 1, 1), S1 - 1);
+  const int nq = min(max(min(num_kv_splits[b], split_cap) - 1, 1), S1 - 1);
   const int64_t row = ((int64_t)b * H + h) * S1;
   float M = -3.0e38f;
 #pragma unroll 8
@@ -925,13 +729,21 @@ static int rolaq_decode_head_groups(int D, int H) {
   return D == 512 ? 1 : (nhg < 3 ? nhg : 3);
 }
 
+int rolaq_decode_head_blocks(int D, int H) {
+  const int HG = rolaq_decode_head_groups(D, H);
+  return ((H + 15) / 16 + HG - 1) / HG;
+}
+
 hipError_t rolaq_launch_decode(const rolaq::DecodeArgs& a, int D, int R, int max_splits,
                                uint16_t* out, int64_t o_sb, int64_t o_sh, int stages,
                                hipStream_t stream) {
   using namespace rolaq;
   const int HG = rolaq_decode_head_groups(D, a.H);
   const int nhb = ((a.H + 15) / 16 + HG - 1) / HG;
-  const dim3 grid(a.B * nhb, max_splits + 1), block(kThreads);
+  // split rows 0 .. nq, nq = min(max(min(ns, cap) - 1, 1), max_splits): the
+  // quantized splits, then the window split's neutral partial
+  const int rows = a.split_cap < max_splits ? (a.split_cap < 2 ? 2 : a.split_cap) : max_splits + 1;
+  const dim3 grid(a.B * nhb, rows), block(kThreads);
 #define ROLAQ_S1(DD, RR, GG) \
   if (D == DD && R == RR && HG == GG) hipLaunchKernelGGL((decode_stage1<DD, RR, GG>), grid, block, 0, stream, a);
   if (stages & kStagePartials) {
@@ -945,10 +757,10 @@ hipError_t rolaq_launch_decode(const rolaq::DecodeArgs& a, int D, int R, int max
   if (stages & kStageMerge) {
     if (D == 512)
       hipLaunchKernelGGL((decode_stage2<512>), dim3(a.B * a.H), dim3(128), 0, stream, a.logits, a.lse,
-                         a.num_kv_splits, a.H, a.S1, out, o_sb, o_sh);
+                         a.num_kv_splits, a.split_cap, a.H, a.S1, out, o_sb, o_sh);
     else if (D == 256)
       hipLaunchKernelGGL((decode_stage2<256>), dim3(a.B * a.H), dim3(128), 0, stream, a.logits, a.lse,
-                         a.num_kv_splits, a.H, a.S1, out, o_sb, o_sh);
+                         a.num_kv_splits, a.split_cap, a.H, a.S1, out, o_sb, o_sh);
     else
       return hipErrorInvalidValue;
   }

@@ -10,24 +10,29 @@
 // chunk's rows enter as the given BF16 keys; attention is causal.
 //
 // Layout of the work: two launches.
-//   gather  every key row of the extended sequences -- [latent | rope] bf16,
-//           INT2 rows dequantized and rounded once -- into the caller's
-//           workspace, sequence b at rows koff_b .. koff_b + prefix_b + q_b - 1
-//           (koff_b = sum over b' < b of prefix_b' + q_b'); HBM-bound, read
-//           once per call instead of once per query block.
+//   gather  every key row of the extended sequences -- [latent | rope], INT2
+//           rows dequantized and rounded to bf16 once -- into the caller's
+//           workspace as fp16 (the same numbers: a bf16 value is exact in fp16
+//           between 2^-17 and 65504), sequence b at rows koff_b .. koff_b +
+//           prefix_b + q_b - 1 (koff_b = sum over b' < b of prefix_b' + q_b');
+//           HBM-bound, read once per call instead of once per query block.
 //   attend  a block takes BM consecutive (token, head) query rows of one
 //           sequence (all heads share the keys: MQA) and walks its keys in
 //           tiles of 64, each copied from the workspace into LDS by the whole
 //           block while the previous tile is consumed (double-buffered, one
 //           barrier per tile). Per wave and tile:
-//   S^T[64 keys, RW rows] = K . Q^T   on MFMA 16x16x32 (Q held in registers);
+//   S^T[64 keys, RW rows] = K . Q^T   on fp16 MFMA 16x16x32 (Q converted to fp16
+//                                     once, held in registers: exact products);
 //   the causal mask only on tiles that reach past the block's first query position
-//   softmax in the log2 domain against a fixed per-row reference (the row's
-//   maximum over the first tile); a block whose scores exceed it by more than
-//   2^64 somewhere is redone with the true maxima, so O is never rescaled
-//   O[RW rows, D] += P . V           on MFMA 16x16x32 per 32-key half, the keys of each lane
-//                                     taken in the order the score MFMA left them,
-//                                     P split into bf16 hi + lo (FP32-level accuracy).
+//   softmax in the log2 domain against a per-row reference (the row's maximum
+//   over the first tile + 8); a tile whose scores pass it by more than 15
+//   moves it to the tile's maximum + 8 and scales O and the row sum by the
+//   difference in place (scale_acc4), so every probability fits fp16
+//   O[RW rows, D] += P . V           on fp16 MFMA 16x16x32 per 32-key half, the keys of
+//                                     each lane taken in the order the score MFMA left
+//                                     them, P rounded to fp16 (relative error 2^-12).
+// A sequence whose key rows do not fit the workspace (the caller's key_rows
+// was short of the true sum) gets NaN outputs.
 #include "rolaq_common.h"
 #include "rolaq_args.h"
 
@@ -36,7 +41,8 @@ namespace rolaq {
 constexpr int kExtKeys = 64;          // keys per tile
 constexpr int kExtMK = kExtKeys / 16;  // 16-key blocks per tile
 constexpr int kExtKH = kExtKeys / 32;  // 32-key halves (K-steps of the output MFMA)
-constexpr float kExtSlack = 64.0f;    // log2 headroom of a score over the softmax reference
+constexpr float kExtSlack = 15.0f;    // max exp2 argument: a probability stays <= 2^15 (fp16)
+constexpr float kExtHeadroom = 8.0f;  // a reference sits this far above the maximum it was set from
 constexpr float kExtMasked = -1.0e30f;
 
 template <int D, int R>
@@ -78,9 +84,9 @@ __device__ __forceinline__ int64_t key_offset(const ExtendArgs& a, int b) {
   return off;
 }
 
-// Key rows of sequence blockIdx.x (one thread per 16-byte chunk, rows strided
-// over blockIdx.y): chunk rows from k_chunk, prefix rows from the BF16 window
-// (t < P or t >= L - W of the extended length L) or the INT2 row
+// Key rows of sequence blockIdx.x as fp16 (one thread per 16-byte chunk, rows
+// strided over blockIdx.y): chunk rows from k_chunk, prefix rows from the BF16
+// window (t < P or t >= L - W of the extended length L) or the INT2 row
 // ((code - zero) * scale rounded to bf16), rope from rope_buf.
 template <int D, int R>
 __global__ __launch_bounds__(256) void extend_gather_kernel(ExtendArgs a) {
@@ -102,14 +108,14 @@ __global__ __launch_bounds__(256) void extend_gather_kernel(ExtendArgs a) {
     const int c = (int)(e - t * CPR);
     u32x4 v;
     if (t >= prefix) {
-      v = gload<u32x4>(a.kc + (qo0 + t - prefix) * a.kc_st + 8 * c);
+      v = bf16x8_to_f16x8(gload<u32x4>(a.kc + (qo0 + t - prefix) * a.kc_st + 8 * c));
     } else {
       const int64_t slot = ((int64_t)a.kv_indices[kv0 + (t >> a.page_shift)] << a.page_shift) + (t & pmask);
       if (c >= D / 8) {
-        v = gload<u32x4>(a.rope + slot * R + 8 * (c - D / 8));
+        v = bf16x8_to_f16x8(gload<u32x4>(a.rope + slot * R + 8 * (c - D / 8)));
       } else if (t < P || t >= L - W) {
         const int64_t inner = t < P ? t : P + (t - P) % (W > 0 ? W : 1);
-        v = gload<u32x4>(a.hp + (1 + req * (P + W) + inner) * D + 8 * c);
+        v = bf16x8_to_f16x8(gload<u32x4>(a.hp + (1 + req * (P + W) + inner) * D + 8 * c));
       } else {
         // elements 8c .. 8c + 7 sit in bytes 2c, 2c + 1 of the packed row
         const uint32_t bits = gload<uint16_t>(a.codes + slot * (D / 4) + 2 * c);
@@ -117,7 +123,8 @@ __global__ __launch_bounds__(256) void extend_gather_kernel(ExtendArgs a) {
         float f[8];
 #pragma unroll
         for (int k = 0; k < 8; ++k) f[k] = (float((bits >> (2 * k)) & 3u) - sz.y) * sz.x;
-        v = u32x4{pack_bf16(f[0], f[1]), pack_bf16(f[2], f[3]), pack_bf16(f[4], f[5]), pack_bf16(f[6], f[7])};
+        v = bf16x8_to_f16x8(
+            u32x4{pack_bf16(f[0], f[1]), pack_bf16(f[2], f[3]), pack_bf16(f[4], f[5]), pack_bf16(f[6], f[7])});
       }
     }
     *reinterpret_cast<u32x4*>(a.ws + (koff + t) * DR + 8 * c) = v;
@@ -143,6 +150,7 @@ template <int D, int R>
 __global__ __launch_bounds__((64 * ExtGeo<D, R>::WAVES), 1) void extend_kernel(ExtendArgs a) {
   using G = ExtGeo<D, R>;
   constexpr int KSQ = G::KSQ, NBR = G::NBR, RW = G::RW, BM = G::BM, ND = G::ND;
+  define_acc_macros();
   extern __shared__ __attribute__((aligned(16))) uint8_t s_buf[];
 
   const int b = blockIdx.x;
@@ -155,18 +163,25 @@ __global__ __launch_bounds__((64 * ExtGeo<D, R>::WAVES), 1) void extend_kernel(E
   const int64_t prefix = a.prefix_lens[b];
   const int64_t L = prefix + Tq;
   const int64_t koff = key_offset(a, b);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int gq = lane >> 4, la = lane & 15;
+  if (koff + L > a.ws_rows) {
+    // the sequence's key rows did not fit the workspace: its outputs are NaN
+    for (int64_t e = tid; e < (int64_t)BM * D; e += 64 * G::WAVES) {
+      const int64_t r = r0 + e / D;
+      if (r < nrows) a.out[(qo0 + r / a.H) * a.o_st + (r % a.H) * a.o_sh + e % D] = 0x7FC0;
+    }
+    return;
+  }
   // last query token of the block -> keys 0 .. prefix + t_last
   const int64_t t_last = min(nrows - 1, r0 + BM - 1) / a.H;
   const int kend = (int)(prefix + t_last + 1);
   const int ntiles = (kend + kExtKeys - 1) / kExtKeys;
 
-  const int tid = threadIdx.x, lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int gq = lane >> 4, la = lane & 15;
   // tile copy: thread tid moves 16-byte chunks tid, tid + NT, ... of the tile's
-  // 32 key rows (keys past the block's last key, or past the workspace, are zeros)
+  // key rows (keys past the block's last key are zeros)
   constexpr int DR = D + R, CPR = DR / 8, CH = kExtKeys * CPR, NT = 64 * G::WAVES, NCH = (CH + NT - 1) / NT;
-  const int64_t krows = min((int64_t)kend, a.ws_rows - koff);
   u32x4 raw[NCH];
   auto load_keys = [&](int k0) {
 #pragma unroll
@@ -174,7 +189,7 @@ __global__ __launch_bounds__((64 * ExtGeo<D, R>::WAVES), 1) void extend_kernel(E
       const int ci = tid + NT * j;
       const int key = ci / CPR, c = ci - key * CPR;
       const int64_t kp = k0 + key;
-      raw[j] = (ci < CH && kp < krows) ? gload<u32x4>(a.ws + (koff + kp) * DR + 8 * c) : u32x4{0u, 0u, 0u, 0u};
+      raw[j] = (ci < CH && kp < kend) ? gload<u32x4>(a.ws + (koff + kp) * DR + 8 * c) : u32x4{0u, 0u, 0u, 0u};
     }
   };
   auto store_keys = [&](uint8_t* buf) {
@@ -186,7 +201,7 @@ __global__ __launch_bounds__((64 * ExtGeo<D, R>::WAVES), 1) void extend_kernel(E
     }
   };
 
-  // ---- query rows of this wave: Q^T fragments and positions -----------------
+  // ---- query rows of this wave: Q^T fragments (fp16) and positions ------------
   u32x4 qf[NBR][KSQ];
   int64_t qpos[NBR];
 #pragma unroll
@@ -198,7 +213,7 @@ __global__ __launch_bounds__((64 * ExtGeo<D, R>::WAVES), 1) void extend_kernel(E
     const uint16_t* qr = a.q + (qo0 + t) * a.q_st + h * a.q_sh + 8 * gq;
 #pragma unroll
     for (int ks = 0; ks < KSQ; ++ks)
-      qf[nb][ks] = ok ? *reinterpret_cast<const u32x4*>(qr + 32 * ks) : u32x4{0u, 0u, 0u, 0u};
+      qf[nb][ks] = ok ? bf16x8_to_f16x8(*reinterpret_cast<const u32x4*>(qr + 32 * ks)) : u32x4{0u, 0u, 0u, 0u};
   }
 
   const float c2 = a.sm_scale * kLog2e;
@@ -208,70 +223,88 @@ __global__ __launch_bounds__((64 * ExtGeo<D, R>::WAVES), 1) void extend_kernel(E
   for (int nb = 0; nb < NBR; ++nb) qp[nb] = (int)qpos[nb];
 
   f32x4 acc_o[NBR][ND];
-  float m_ref[NBR], m_lane[NBR], l_run[NBR];
-  bool redo = false;
-  for (int pass = 0; pass < 2; ++pass) {
+  float m_ref[NBR], l_run[NBR];
 #pragma unroll
-    for (int nb = 0; nb < NBR; ++nb) {
+  for (int nb = 0; nb < NBR; ++nb) {
 #pragma unroll
-      for (int nd = 0; nd < ND; ++nd) acc_o[nb][nd] = f32x4{0.f, 0.f, 0.f, 0.f};
-      m_lane[nb] = kExtMasked;
-      l_run[nb] = 0.f;
+    for (int nd = 0; nd < ND; ++nd) acc_o[nb][nd] = f32x4{0.f, 0.f, 0.f, 0.f};
+    m_ref[nb] = kExtMasked;
+    l_run[nb] = 0.f;
+  }
+
+  load_keys(0);
+  store_keys(s_buf);
+  __syncthreads();
+
+  for (int it = 0; it < ntiles; ++it) {
+    const uint8_t* kb = s_buf + (it & 1) * G::BUF;
+    const int k0 = it * kExtKeys;
+    // loads of the next tile first: they have this tile's compute to land
+    if (it + 1 < ntiles) load_keys(k0 + kExtKeys);
+
+    // ---- scores S^T[key, row] ----------------------------------------------
+    f32x4 s[kExtMK][NBR];
+#pragma unroll
+    for (int mk = 0; mk < kExtMK; ++mk)
+#pragma unroll
+      for (int nb = 0; nb < NBR; ++nb) s[mk][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < KSQ; ++ks) {
+#pragma unroll
+      for (int mk = 0; mk < kExtMK; ++mk) {
+        const u32x4 kf = *reinterpret_cast<const u32x4*>(kb + (16 * mk + la) * G::KSTR + 64 * ks + 16 * gq);
+#pragma unroll
+        for (int nb = 0; nb < NBR; ++nb) s[mk][nb] = mfma16x16x32_f16(kf, qf[nb][ks], s[mk][nb]);
+      }
     }
 
-    load_keys(0);
-    store_keys(s_buf);
-    __syncthreads();
-
-    for (int it = 0; it < ntiles; ++it) {
-      const uint8_t* kb = s_buf + (it & 1) * G::BUF;
-      const int k0 = it * kExtKeys;
-      // loads of the next tile first: they have this tile's compute to land
-      if (it + 1 < ntiles) load_keys(k0 + kExtKeys);
-
-      // ---- scores S^T[key, row] --------------------------------------------
-      f32x4 s[kExtMK][NBR];
+    // ---- softmax (row = 16 nb + la; keys 16 mk + 4 gq + i) -------------------
+    // A tile that ends before the block's first query position needs no mask
+    // (rows past the last query, qp = -1, stay masked).
+    const bool open = k0 + kExtKeys - 1 <= qfirst;
+    float mx[NBR];
+    uint64_t need[NBR];  // lanes whose row passes its reference by more than the slack
+#pragma unroll
+    for (int nb = 0; nb < NBR; ++nb) {
+      mx[nb] = kExtMasked;
 #pragma unroll
       for (int mk = 0; mk < kExtMK; ++mk)
 #pragma unroll
-        for (int nb = 0; nb < NBR; ++nb) s[mk][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int ks = 0; ks < KSQ; ++ks) {
-#pragma unroll
-        for (int mk = 0; mk < kExtMK; ++mk) {
-          const u32x4 kf = *reinterpret_cast<const u32x4*>(kb + (16 * mk + la) * G::KSTR + 64 * ks + 16 * gq);
-#pragma unroll
-          for (int nb = 0; nb < NBR; ++nb) s[mk][nb] = mfma16x16x32(kf, qf[nb][ks], s[mk][nb]);
+        for (int i = 0; i < 4; ++i) {
+          const int kp = k0 + 16 * mk + 4 * gq + i;
+          const float v = ((open && qp[nb] >= 0) || kp <= qp[nb]) ? s[mk][nb][i] * c2 : kExtMasked;
+          s[mk][nb][i] = v;
+          mx[nb] = fmaxf(mx[nb], v);
         }
+      need[nb] = __builtin_amdgcn_ballot_w64(it > 0 && mx[nb] > m_ref[nb] + kExtSlack);
+    }
+    // the first tile sets each row's reference (key 0 is visible to every row)
+    if (it == 0) {
+#pragma unroll
+      for (int nb = 0; nb < NBR; ++nb) m_ref[nb] = max_over_rows(mx[nb]) + kExtHeadroom;
+    }
+    // rows past the slack: reference to the tile's maximum + 8, O and the sum
+    // scaled by the difference (O's lane holds rows 4 gq + i, whose factors
+    // come from the lanes whose row la is that row)
+#pragma unroll
+    for (int nb = 0; nb < NBR; ++nb) {
+      float fj[4] = {1.f, 1.f, 1.f, 1.f};
+      if (need[nb]) {
+        const float mt = max_over_rows(mx[nb]);
+        const float mn = mt > m_ref[nb] + kExtSlack ? mt + kExtHeadroom : m_ref[nb];
+        const float f = __builtin_amdgcn_exp2f(m_ref[nb] - mn);
+        l_run[nb] *= f;
+        m_ref[nb] = mn;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) fj[i] = __shfl(f, 4 * gq + i);
       }
-
-      // ---- softmax against the fixed reference (row = 16 nb + la; keys 16 mk + 4 gq + i)
-      // A tile that ends before the block's first query position needs no mask
-      // (rows past the last query, qp = -1, stay masked: no scores, no redo).
-      const bool open = k0 + kExtKeys - 1 <= qfirst;
 #pragma unroll
-      for (int nb = 0; nb < NBR; ++nb) {
-        float mx = m_lane[nb];
+      for (int nd = 0; nd < ND; nd += 4)
+        scale_acc4(acc_o[nb][nd], acc_o[nb][nd + 1], acc_o[nb][nd + 2], acc_o[nb][nd + 3], fj, need[nb]);
+    }
+    u32x4 pf[kExtKH][NBR];
 #pragma unroll
-        for (int mk = 0; mk < kExtMK; ++mk)
-#pragma unroll
-          for (int i = 0; i < 4; ++i) {
-            const int kp = k0 + 16 * mk + 4 * gq + i;
-            const float v = ((open && qp[nb] >= 0) || kp <= qp[nb]) ? s[mk][nb][i] * c2 : kExtMasked;
-            s[mk][nb][i] = v;
-            mx = fmaxf(mx, v);
-          }
-        m_lane[nb] = mx;
-      }
-      // the reference of the first pass: each row's maximum over the first tile
-      // (key 0 is visible to every row, so it is finite)
-      if (it == 0 && pass == 0) {
-#pragma unroll
-        for (int nb = 0; nb < NBR; ++nb) m_ref[nb] = max_over_rows(m_lane[nb]);
-      }
-      u32x4 pf[kExtKH][NBR], pl[kExtKH][NBR];
-#pragma unroll
-      for (int kh = 0; kh < kExtKH; ++kh)
+    for (int kh = 0; kh < kExtKH; ++kh)
 #pragma unroll
       for (int nb = 0; nb < NBR; ++nb) {
         float p[2][4];
@@ -282,51 +315,25 @@ __global__ __launch_bounds__((64 * ExtGeo<D, R>::WAVES), 1) void extend_kernel(E
             p[mk][i] = __builtin_amdgcn_exp2f(s[2 * kh + mk][nb][i] - m_ref[nb]);  // masked: 2^-1e30 = 0
             l_run[nb] += p[mk][i];
           }
-        // P as bf16 hi + lo: the output keeps FP32-level accuracy in P
-        pf[kh][nb] = u32x4{pack_bf16(p[0][0], p[0][1]), pack_bf16(p[0][2], p[0][3]), pack_bf16(p[1][0], p[1][1]),
-                           pack_bf16(p[1][2], p[1][3])};
-        float r[2][4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const uint32_t w = pf[kh][nb][e];
-          r[e >> 1][2 * (e & 1)] = p[e >> 1][2 * (e & 1)] - bf16_lo(w);
-          r[e >> 1][2 * (e & 1) + 1] = p[e >> 1][2 * (e & 1) + 1] - bf16_hi(w);
-        }
-        pl[kh][nb] = u32x4{pack_bf16(r[0][0], r[0][1]), pack_bf16(r[0][2], r[0][3]), pack_bf16(r[1][0], r[1][1]),
-                           pack_bf16(r[1][2], r[1][3])};
+        pf[kh][nb] = u32x4{pack_f16(p[0][0], p[0][1]), pack_f16(p[0][2], p[0][3]), pack_f16(p[1][0], p[1][1]),
+                           pack_f16(p[1][2], p[1][3])};
       }
 
-      // ---- O[row, d] += P . V ------------------------------------------------
+    // ---- O[row, d] += P . V --------------------------------------------------
 #pragma unroll
-      for (int kh = 0; kh < kExtKH; ++kh)
+    for (int kh = 0; kh < kExtKH; ++kh)
 #pragma unroll
       for (int nd = 0; nd < ND; ++nd) {
         const uint8_t* kv = kb + 32 * kh * G::KSTR;
         const u32x2 v0 = read_v_tr(kv, G::KSTR, gq, la, nd, 0), v1 = read_v_tr(kv, G::KSTR, gq, la, nd, 1);
         const u32x4 vf = {v0.x, v0.y, v1.x, v1.y};
 #pragma unroll
-        for (int nb = 0; nb < NBR; ++nb) {
-          acc_o[nb][nd] = mfma16x16x32(pf[kh][nb], vf, acc_o[nb][nd]);
-          acc_o[nb][nd] = mfma16x16x32(pl[kh][nb], vf, acc_o[nb][nd]);
-        }
+        for (int nb = 0; nb < NBR; ++nb) acc_o[nb][nd] = mfma16x16x32_f16(pf[kh][nb], vf, acc_o[nb][nd]);
       }
 
-      // ---- next tile into the other buffer (last read before the previous barrier)
-      if (it + 1 < ntiles) store_keys(s_buf + ((it + 1) & 1) * G::BUF);
-      __syncthreads();
-    }
-
-    // a score above the reference by more than the slack (2^64 bounds every P
-    // and keeps the sums finite): redo the block with each row's true maximum
-    bool over = false;
-#pragma unroll
-    for (int nb = 0; nb < NBR; ++nb) {
-      const float mt = max_over_rows(m_lane[nb]);
-      over |= mt > m_ref[nb] + kExtSlack;
-      m_ref[nb] = mt;
-    }
-    redo = __syncthreads_or(pass == 0 && over);
-    if (!redo) break;
+    // ---- next tile into the other buffer (last read before the previous barrier)
+    if (it + 1 < ntiles) store_keys(s_buf + ((it + 1) & 1) * G::BUF);
+    __syncthreads();
   }
 
   // ---- normalise and store -----------------------------------------------------

@@ -18,6 +18,7 @@ struct DecodeArgs {
   const int64_t* seq_lens;
   const int64_t* req_idx;
   const int32_t* num_kv_splits;
+  int split_cap;  // request b uses min(num_kv_splits[b], split_cap) splits
   int S1;        // max_kv_splits + 1
   int max_reqs;  // requests with ring rows; req_idx outside [0, max_reqs) reads no window rows
   int B, H, P, W;
@@ -116,6 +117,8 @@ struct AssembleArgs {
 constexpr int kStagePartials = 1, kStageMerge = 2;
 hipError_t rolaq_launch_decode(const rolaq::DecodeArgs& a, int D, int R, int max_splits, uint16_t* out,
                                int64_t o_sb, int64_t o_sh, int stages, hipStream_t stream);
+// Blocks of 16 * head-groups heads that one (sequence, split) of decode launches.
+int rolaq_decode_head_blocks(int D, int H);
 // Device address, on the current device, of the allocation-free decode's
 // static workspace of kNoAllocScratchBytes bytes (looked up once per device).
 constexpr size_t kNoAllocScratchBytes = size_t(32) << 20;

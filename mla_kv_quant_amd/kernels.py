@@ -244,7 +244,10 @@ def decode_fwd(q: torch.Tensor, codes: torch.Tensor, params: torch.Tensor, rope_
     """Absorbed decode over the packed cache: ``q [B, H, D+R]`` -> ``out [B, H, D]``.
 
     ``max_reqs``: requests with ring rows in ``hp_c`` (default: as many as its
-    rows hold); a ``req_idx`` outside ``[0, max_reqs)`` reads no window rows."""
+    rows hold); a ``req_idx`` outside ``[0, max_reqs)`` reads no window rows.
+    Request ``b`` uses ``min(num_kv_splits[b], decode_split_cap(...))`` splits
+    (about one working block per compute unit); the partials in
+    ``attn_logits``/``attn_lse`` follow that count."""
     B, H, D, R = _decode_check(q, codes, params, rope_buf, hp_c, kv_indptr, kv_indices, seq_lens, req_idx,
                                num_kv_splits, max_kv_splits, attn_logits, attn_lse)
     _out_check(out, B, H, D, q.device)
@@ -255,6 +258,15 @@ def decode_fwd(q: torch.Tensor, codes: torch.Tensor, params: torch.Tensor, rope_
         int(max_kv_splits), B, H, D, R, int(P), int(W), float(sm_scale), _p(attn_logits),
         _p(attn_lse), _p(out), out.stride(0), out.stride(1), _stream(q)))
     return out
+
+
+def decode_split_cap(B: int, H: int, D: int, max_kv_splits: int) -> int:
+    """The most splits :func:`decode_fwd` gives one request on the current
+    device: enough quantized splits for one working block per compute unit
+    over the batch, plus the window split, at most ``max_kv_splits``."""
+    cap = ctypes.c_int(0)
+    _lib.check(_lib.load().rolaq_decode_split_cap(int(B), int(H), int(D), int(max_kv_splits), ctypes.byref(cap)))
+    return cap.value
 
 
 def decode_partials(q: torch.Tensor, codes: torch.Tensor, params: torch.Tensor, rope_buf: torch.Tensor,
@@ -294,13 +306,17 @@ def extend_fwd(q: torch.Tensor, k_chunk: torch.Tensor, qo_indptr: torch.Tensor, 
                kv_indices: torch.Tensor, prefix_lens: torch.Tensor, req_idx: torch.Tensor, codes: torch.Tensor,
                params: torch.Tensor, rope_buf: torch.Tensor, hp_c: torch.Tensor, max_q_len: int,
                out: torch.Tensor, sm_scale: float, P: int, W: int, page_size: int = 1,
-               max_reqs: int | None = None, workspace: torch.Tensor | None = None) -> torch.Tensor:
+               max_reqs: int | None = None, workspace: torch.Tensor | None = None,
+               key_rows: int | None = None) -> torch.Tensor:
     """Causal extend over the packed prefix + the chunk: ``q [T, H, D+R]`` -> ``out [T, H, D]``.
 
-    ``max_reqs`` as for :func:`decode_fwd`. ``workspace``: bf16
-    ``[rows, D + R]`` with ``rows >= sum(prefix_lens) + T`` (the key rows of
-    the extended sequences are gathered into it); allocated here when not
-    given, which reads ``prefix_lens`` back to the host."""
+    ``max_reqs`` as for :func:`decode_fwd`. ``key_rows``: the number of key
+    rows of the extended sequences, ``sum(prefix_lens) + T``, as the caller
+    knows it on the host (SGLang: ``extend_prefix_lens_cpu`` and the token
+    count); read back from the device when not given (one host sync).
+    ``workspace``: 16-bit ``[rows, D + R]`` scratch (bf16 or fp16 storage;
+    fp16 values are written into it) with ``rows >= key_rows``, allocated
+    here when not given; a shorter one raises ``ValueError``."""
     dev = q.device
     _need(q, "q", torch.bfloat16, dev, 3)
     T, H, DR = q.shape
@@ -331,10 +347,12 @@ def extend_fwd(q: torch.Tensor, k_chunk: torch.Tensor, qo_indptr: torch.Tensor, 
     if out.shape[0] < T or tuple(out.shape[1:]) != (H, D) or out.stride(2) != 1:
         raise ValueError("out must be [T, H, D] with a contiguous last dim")
     mr = _ring_reqs(hp_c, P, W, max_reqs)
+    if key_rows is None:
+        key_rows = int(prefix_lens[:B].sum().item()) + int(qo_indptr[B].item()) - int(qo_indptr[0].item())
     if workspace is None:
-        rows = int(prefix_lens[:B].sum().item()) + int(qo_indptr[B].item()) - int(qo_indptr[0].item())
-        workspace = torch.empty(max(rows, 1), DR, dtype=torch.bfloat16, device=dev)
-    _need(workspace, "workspace", torch.bfloat16, dev, 2)
+        workspace = torch.empty(max(int(key_rows), 1), DR, dtype=torch.float16, device=dev)
+    if workspace.dtype not in (torch.bfloat16, torch.float16) or workspace.device != dev or workspace.dim() != 2:
+        raise TypeError("workspace must be a 2-D bf16 or fp16 tensor on the query's device")
     _contig(workspace, "workspace")
     if workspace.shape[1] != DR:
         raise ValueError("workspace must be [rows, D + R]")
@@ -342,7 +360,7 @@ def extend_fwd(q: torch.Tensor, k_chunk: torch.Tensor, qo_indptr: torch.Tensor, 
         _p(q), q.stride(0), q.stride(1), _p(k_chunk), k_chunk.stride(0), _p(qo_indptr), _p(kv_indptr),
         _p(kv_indices), int(page_size), _p(prefix_lens), _p(req_idx), mr, _p(codes), _p(params), _p(rope_buf),
         _p(hp_c), B, H, D, R, int(P), int(W), int(max_q_len), float(sm_scale), _p(workspace),
-        workspace.shape[0], _p(out), out.stride(0), out.stride(1), _stream(q)))
+        workspace.shape[0], int(key_rows), _p(out), out.stride(0), out.stride(1), _stream(q)))
     return out
 
 

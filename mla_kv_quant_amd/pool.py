@@ -57,6 +57,19 @@ class PackedMLAPool:
         rotations = rotations or [None] * layer_num
         self.rotations = [None if r is None else r.to(device=dev, dtype=dtype) for r in rotations]
         self._rolaq_quantizers = list(quantizers) if quantizers is not None else [None] * layer_num
+        self._extend_ws = None  # the extend reader's key-row workspace, shared by all layers
+
+    def extend_workspace(self, rows: int) -> torch.Tensor:
+        """The extend reader's scratch of at least ``rows`` key rows (fp16
+        ``[rows, D + R]``): one buffer for every layer and call, reallocated
+        only when a batch needs more rows than it holds."""
+        need = max(int(rows), 1)
+        ws = self._extend_ws
+        if ws is None or ws.shape[0] < need:
+            ws = torch.empty(need, self.kv_lora_rank + self.qk_rope_head_dim, dtype=torch.float16,
+                             device=self.device)
+            self._extend_ws = ws
+        return ws
 
     def latent_rotation(self, layer_id: int, local: bool = True):
         li = layer_id - self.start_layer if local else layer_id

@@ -160,7 +160,7 @@ def extend(pool: dict, q_lat, q_rope, chunk_lat, chunk_rope, prefix_slots, prefi
            req: int, P: int, W: int, sm_scale: float, width: int, chunk_mode: str = "bf16",
            rotation=None, threshold: float = codec.LLOYD_MAX_THRESHOLD,
            gain: float = codec.LLOYD_MAX_STRETCH, dtype=torch.float32, max_reqs: int | None = None,
-           rows=None):
+           rows=None, flavour: str = "fp"):
     """Causal extend attention of one sequence: ``Tq`` new queries at positions
     ``prefix_len ..`` over the packed prefix plus the chunk itself. A request
     outside ``[0, max_reqs)`` has no window rows (``P = W = 0``).
@@ -170,6 +170,8 @@ def extend(pool: dict, q_lat, q_rope, chunk_lat, chunk_rope, prefix_slots, prefi
     ``chunk_mode="qdq"`` (HF semantics, cache.py:1030-1039): chunk rows outside
     the last ``W`` positions are Lloyd-QDQ'd (rounded to bf16) before attention.
     ``rows``: evaluate only the queries of these chunk rows (returns ``[len(rows), H, D]``).
+    ``flavour="bf16_eager"``: the reference model's attention in bf16
+    (:func:`attend_bf16_eager`; returns ``(out, None)``) instead of ``dtype``.
     """
     if max_reqs is not None and not 0 <= int(req) < int(max_reqs):
         P = W = 0
@@ -202,6 +204,8 @@ def extend(pool: dict, q_lat, q_rope, chunk_lat, chunk_rope, prefix_slots, prefi
     if rows is not None:  # only these chunk rows' queries (the keys are the whole chunk's)
         rows = torch.as_tensor(rows, dtype=torch.long)
         q_lat, q_rope, qpos = q_lat[rows], q_rope[rows], qpos[rows]
+    if flavour == "bf16_eager":
+        return attend_bf16_eager(q_lat, q_rope, k_lat, k_rope, sm_scale, mask=kpos <= qpos), None
     return attend(q_lat, q_rope, k_lat, k_rope, sm_scale, dtype, mask=kpos <= qpos)
 
 

@@ -130,3 +130,21 @@ def gpu_written_pool(lengths, D, R, P, W, page, seed, max_reqs=None, reqs=None, 
                            gp["row_of_slot"], gp["owner_of_row"], P, W, max_reqs, 0.9810652732849121, 1.16)
         torch.cuda.synchronize()
     return gp, slots, pages, reqs
+
+
+def fused_splits(splits, H, D, max_splits):
+    """The split counts rolaq_decode_fwd uses for a batch that requests
+    ``splits``: each capped at the library's split cap for (B, H, D) on the
+    current device (whose partials the fused call writes)."""
+    from mla_kv_quant_amd import kernels
+    cap = kernels.decode_split_cap(len(splits), H, D, max_splits)
+    return [min(int(ns), cap) for ns in splits]
+
+
+def rotated_latent(n, D, outliers, seed, rotation):
+    """bf16 ``[n, D]`` latent rows in a layer's rotated frame: synthetic rows
+    (N(0,1), ``outliers`` channels x20) times ``R_eff = fp32(bf16(R))``, the
+    frame the cache stores and the extend reader's chunk keys live in
+    (mla_quant/quantizer.py:117-118)."""
+    x = synth.make_latent(n, D, outliers, seed=seed).float()
+    return (x @ rotation.to(torch.bfloat16).float()).to(torch.bfloat16)

@@ -19,7 +19,7 @@ def declared_symbols():
 def test_header_declares_the_entry_points():
     syms = declared_symbols()
     for name in ("rolaq_last_error", "rolaq_abi_version", "rolaq_scatter_pack_rows", "rolaq_write_rows",
-                 "rolaq_norm_write_rows", "rolaq_prepare_gf_splits", "rolaq_decode_fwd", "rolaq_decode_partials", "rolaq_decode_merge", "rolaq_extend_fwd",
+                 "rolaq_norm_write_rows", "rolaq_prepare_gf_splits", "rolaq_decode_fwd", "rolaq_decode_partials", "rolaq_decode_merge", "rolaq_decode_split_cap", "rolaq_extend_fwd",
                  "rolaq_assemble_rows"):
         assert name in syms
 
@@ -30,7 +30,7 @@ def test_library_exports_every_declared_symbol():
         assert hasattr(lib, name), name
     # every declared symbol has a ctypes signature in the binding
     assert set(declared_symbols()) - {"rolaq_last_error"} <= set(_lib.SIGNATURES)
-    assert lib.rolaq_abi_version() == 3
+    assert lib.rolaq_abi_version() == 4
 
 
 def test_invalid_arguments_are_rejected_before_any_launch():
@@ -94,7 +94,7 @@ def test_invalid_arguments_are_rejected_before_any_launch():
     assert lib.rolaq_norm_write_rows(*bad) == _lib.ROLAQ_ERR_INVALID and b"(D, R)" in lib.rolaq_last_error()
     # extend: shape and pointer checks, empty batch is a no-op
     eargs = [p, 40 * 288, 288, p, 288, p, p, p, 16, p, p, 4, p, p, p, p, 4, 40, 256, 32, 4, 16, 2048, 0.1, p, 1,
-             p, 40 * 256, 256, None]
+             1, p, 40 * 256, 256, None]
     bad = list(eargs)
     bad[18], bad[19] = 384, 32
     assert lib.rolaq_extend_fwd(*bad) == _lib.ROLAQ_ERR_INVALID and b"(D, R)" in lib.rolaq_last_error()
@@ -113,6 +113,18 @@ def test_invalid_arguments_are_rejected_before_any_launch():
     bad = list(eargs)
     bad[25] = 0
     assert lib.rolaq_extend_fwd(*bad) == _lib.ROLAQ_ERR_INVALID and b"workspace" in lib.rolaq_last_error()
+    bad = list(eargs)
+    bad[26] = 2  # more key rows than the workspace holds
+    assert lib.rolaq_extend_fwd(*bad) == _lib.ROLAQ_ERR_INVALID and b"short" in lib.rolaq_last_error()
+    bad = list(eargs)
+    bad[26] = -1
+    assert lib.rolaq_extend_fwd(*bad) == _lib.ROLAQ_ERR_INVALID
+    # decode split cap: argument checks (a valid call reads the device's CU count)
+    cap = ctypes.c_int(-7)
+    assert lib.rolaq_decode_split_cap(0, 16, 512, 129, ctypes.byref(cap)) == _lib.ROLAQ_ERR_INVALID
+    assert lib.rolaq_decode_split_cap(32, 16, 384, 129, ctypes.byref(cap)) == _lib.ROLAQ_ERR_INVALID
+    assert lib.rolaq_decode_split_cap(32, 16, 512, 129, None) == _lib.ROLAQ_ERR_INVALID
+    assert cap.value == -7
     bad = list(eargs)
     bad[16] = 0
     assert lib.rolaq_extend_fwd(*bad) == _lib.ROLAQ_OK

@@ -96,6 +96,36 @@ def test_decode_flavours_agree():
     assert torch.allclose(oe.double(), o64, rtol=5e-2, atol=1e-2)
 
 
+@pytest.mark.parametrize("T,L,causal", [(1, 70, False), (9, 40, True)])
+def test_bf16_eager_equals_transformers_eager_attention(T, L, causal):
+    """attend_bf16_eager is the reference model's attention in bf16: transformers'
+    eager_attention_forward (models/deepseek_v2/modeling_deepseek_v2.py, the
+    function the reference's HF path runs) with the absorbed query, one shared
+    key/value head repeated over the heads (MQA), bit for bit."""
+    from types import SimpleNamespace
+
+    from transformers.models.deepseek_v2.modeling_deepseek_v2 import eager_attention_forward
+
+    D, R, H, sm = 64, 16, 5, 0.13
+    ql = synth.make_normal((T, H, D), 31, std=1.3)
+    qr = synth.make_normal((T, H, R), 32, std=1.3)
+    kl = synth.make_latent(L, D, 2, seed=33).float()
+    kr = synth.make_normal((L, R), 34).float()
+    mask = None
+    if causal:
+        mask = torch.arange(L)[None, :] <= torch.arange(L - T, L)[:, None]
+    ours = attention.attend_bf16_eager(ql, qr, kl, kr, sm, mask=mask)
+    query = torch.cat([ql, qr], -1).to(torch.bfloat16).transpose(0, 1)[None]  # [1, H, T, D + R]
+    key = torch.cat([kl, kr], -1).to(torch.bfloat16)[None, None]              # [1, 1, L, D + R]
+    value = kl.to(torch.bfloat16)[None, None]                                  # [1, 1, L, D]
+    add = None
+    if mask is not None:
+        add = torch.zeros(1, 1, T, L, dtype=torch.bfloat16).masked_fill(~mask[None, None], float("-inf"))
+    module = SimpleNamespace(num_key_value_groups=H, training=False)
+    ref, _ = eager_attention_forward(module, query, key, value, add, sm)
+    assert torch.equal(ours, ref[0])
+
+
 def test_extend_causal_and_window():
     D, R, P, W, H = 256, 32, 4, 16, 2
     prefix, Tq = 40, 8
