@@ -20,6 +20,7 @@
 #include "rolaq_args.h"
 
 #include <cstddef>
+#include <type_traits>
 
 namespace rolaq {
 
@@ -82,7 +83,11 @@ __device__ __forceinline__ u32x4 rms_apply8(u32x4 v, float r, u32x4 gm) {
 
 
 // A field of the kernel's WriterArgs argument, loaded from the kernel argument
-// segment where it is used (the argument sits at offset 0).
+// segment where it is used. This relies on WriterArgs being writer_kernel's only
+// explicit argument (so it sits at offset 0 of the segment) with the host's
+// layout: both are checked at compile time (here and after writer_kernel).
+static_assert(std::is_standard_layout<WriterArgs>::value && std::is_trivially_copyable<WriterArgs>::value,
+              "kernarg_field reads WriterArgs fields by offsetof");
 template <typename T>
 __device__ __forceinline__ T kernarg_field(size_t off) {
   const auto k = (const __attribute__((address_space(4))) char*)__builtin_amdgcn_kernarg_segment_ptr();
@@ -378,6 +383,11 @@ __global__ __launch_bounds__(64 * kWriterWaves, 1) void writer_kernel(WriterArgs
     }
   }
 }
+
+// kernarg_field: WriterArgs must stay writer_kernel's one explicit argument
+static_assert(std::is_same<decltype(&writer_kernel<512, false>), void (*)(WriterArgs)>::value &&
+                  std::is_same<decltype(&writer_kernel<256, true>), void (*)(WriterArgs)>::value,
+              "writer_kernel's only argument must be WriterArgs (read at kernel-argument offset 0)");
 
 }  // namespace rolaq
 

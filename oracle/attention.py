@@ -156,6 +156,29 @@ def split_partials(q_lat, q_rope, k_lat, k_rope, sm_scale: float, bounds, dtype=
     return torch.stack(parts, -2), torch.stack(lses, -1)
 
 
+def chunk_rows(chunk_lat, prefix_len: int, P: int, W: int, chunk_mode: str = "bf16",
+               threshold: float = codec.LLOYD_MAX_THRESHOLD, gain: float = codec.LLOYD_MAX_STRETCH):
+    """The chunk's key rows (FP32) as the extend attention sees them.
+
+    ``"bf16"``: the given rows (SGLang extend semantics, rolaq_sglang.patch:208-235).
+    ``"qdq"`` (HF semantics, mla_quant/cache.py:1028-1039: the chunk is written
+    to the cache before attention): rows of the extended sequence's window
+    (first ``P`` / last ``W`` positions) are its BF16 rows, the others the
+    Lloyd QDQ of the row (``chunk_lat`` in FP32, the rotated latent) rounded to
+    bf16, as the cache stores them (oscar.py:120-144, quantizer.py:117-120).
+    """
+    c_lat = chunk_lat.float()
+    if chunk_mode == "qdq":
+        L = prefix_len + c_lat.shape[0]
+        pos = np.arange(prefix_len, L)
+        quant = torch.from_numpy(~window.positional_bf16(pos, L, P, W))
+        c_lat = c_lat.to(torch.bfloat16).float()
+        if quant.any():
+            _, _, _, qdq = codec.lloyd_codec(chunk_lat.float()[quant], codec.GROUP_SIZE, threshold, gain)
+            c_lat[quant] = qdq.to(torch.bfloat16).float()
+    return c_lat
+
+
 def extend(pool: dict, q_lat, q_rope, chunk_lat, chunk_rope, prefix_slots, prefix_len: int,
            req: int, P: int, W: int, sm_scale: float, width: int, chunk_mode: str = "bf16",
            rotation=None, threshold: float = codec.LLOYD_MAX_THRESHOLD,
@@ -167,8 +190,9 @@ def extend(pool: dict, q_lat, q_rope, chunk_lat, chunk_rope, prefix_slots, prefi
 
     ``chunk_mode="bf16"`` (SGLang extend semantics, rolaq_sglang.patch:208-235):
     the chunk's own rows enter as the given BF16 rotated latent.
-    ``chunk_mode="qdq"`` (HF semantics, cache.py:1030-1039): chunk rows outside
-    the last ``W`` positions are Lloyd-QDQ'd (rounded to bf16) before attention.
+    ``chunk_mode="qdq"`` (HF semantics, cache.py:1028-1039): chunk rows outside
+    the window are Lloyd-QDQ'd (rounded to bf16) before attention, window rows
+    rounded to bf16 (:func:`chunk_rows`).
     ``rows``: evaluate only the queries of these chunk rows (returns ``[len(rows), H, D]``).
     ``flavour="bf16_eager"``: the reference model's attention in bf16
     (:func:`attend_bf16_eager`; returns ``(out, None)``) instead of ``dtype``.
@@ -189,14 +213,7 @@ def extend(pool: dict, q_lat, q_rope, chunk_lat, chunk_rope, prefix_slots, prefi
             # rows that left the window are read back from their INT2 codes
             lat_q, _ = gather_rows(pool, prefix_slots, req, prefix_len, 0, 0, width)
             lat_p[leave] = lat_q[leave]
-    c_lat = chunk_lat.float()
-    if chunk_mode == "qdq":
-        pos = np.arange(prefix_len, L)
-        quant = torch.from_numpy(~window.positional_bf16(pos, L, P, W))
-        if quant.any():
-            _, _, _, qdq = codec.lloyd_codec(c_lat[quant], codec.GROUP_SIZE, threshold, gain)
-            c_lat = c_lat.clone()
-            c_lat[quant] = qdq.to(torch.bfloat16).float()
+    c_lat = chunk_rows(chunk_lat, prefix_len, P, W, chunk_mode, threshold, gain)
     k_lat = torch.cat([lat_p, c_lat], 0)
     k_rope = torch.cat([rope_p, chunk_rope.float()], 0)
     qpos = torch.arange(prefix_len, L)[:, None]

@@ -27,6 +27,8 @@ CASES = [
     ("minicpm3_paged32", 256, 32, 40, [513, 64], [130, 1], 32),
     ("dsv2_h16_tokens", 512, 64, 16, [200, 37], [33, 64], 1),
     ("dsv2_h8_paged64", 512, 64, 8, [640, 129], [17, 90], 64),
+    ("dsv3_h128", 512, 64, 128, [300, 40], [20, 7], 64),        # eight head blocks
+    ("minicpm3_h64", 256, 32, 64, [90, 700], [12, 33], 64),
 ]
 
 
@@ -69,12 +71,14 @@ def run_case(D, R, H, prefixes, chunks, page, seed, rope_scale=1.0, P=4, W=16, m
 WINDOWS = [(4, 16), (4, 8), (0, 0)]  # s4r16, s4r8, nowin (mla_quant/common.py:16)
 
 
-@pytest.mark.parametrize("win", WINDOWS, ids=[f"P{p}W{w}" for p, w in WINDOWS])
-@pytest.mark.parametrize("case", CASES, ids=[c[0] for c in CASES])
+# every case with s4r16; s4r8 and nowin on token slots, a partial head group and many head blocks
+ALL_WINDOWS = ("minicpm3_h40", "dsv2_h16_tokens", "dsv3_h128", "minicpm3_h64")
+PAIRS = [(c, w) for w in WINDOWS for c in CASES if w == (4, 16) or c[0] in ALL_WINDOWS]
+
+
+@pytest.mark.parametrize("case,win", PAIRS, ids=[f"{c[0]}-P{w[0]}W{w[1]}" for c, w in PAIRS])
 def test_extend_matches_oracle(case, win):
     name, D, R, H, prefixes, chunks, page = case
-    if win != (4, 16) and name not in ("minicpm3_h40", "dsv2_h16_tokens"):
-        pytest.skip("other window presets run on a representative subset")
     out, ref = run_case(D, R, H, prefixes, chunks, page, seed=7 + len(name), P=win[0], W=win[1])
     assert torch.isfinite(out).all()
     torch.testing.assert_close(out.double(), ref, rtol=RTOL, atol=ATOL)
@@ -194,3 +198,50 @@ def test_extend_short_workspace():
     torch.cuda.synchronize()
     assert torch.equal(got[:chunks[0]], ok.float().cpu()[:chunks[0]])  # the first sequence fits: same output
     assert torch.isfinite(ok.float()).all()
+
+
+def test_extend_hf_chunk_semantics():
+    """HF cache semantics (mla_quant/cache.py:1028-1039): the chunk is written
+    into the cache before attention, so its rows outside the extended
+    sequence's window enter as their Lloyd QDQ rounded to bf16 and its window
+    rows as BF16. With the whole extended sequences in the cache (written by
+    the oracle's writer), the dequantize-rows kernel reads the chunk's stored
+    rows back, in the rotated frame, bit for bit equal to the oracle's
+    chunk_rows(..., "qdq") of the chunk's FP32 rotated latent; fed to the
+    extend reader as the chunk's keys they give the output of
+    oracle.attention.extend(chunk_mode="qdq") at the attention bar."""
+    from oracle import codec
+
+    D, R, H, page, P, W = 256, 32, 16, 16, 4, 16
+    prefixes, chunks = [200, 37], [40, 9]  # the second chunk is shorter than W: prefix rows stay in the window
+    lengths = [p + c for p, c in zip(prefixes, chunks)]
+    sm = 1.0 / math.sqrt(96)
+    seed = 23
+    pool, slots, pages, reqs, rot = build_pool(lengths, D, R, P, W, page, seed=seed)
+    gp = pool_to_gpu(pool)
+    B, T = len(prefixes), sum(chunks)
+    chunk_slots = np.concatenate([slots[b][prefixes[b]:lengths[b]] for b in range(B)]).astype(np.int64)
+    kc = torch.empty(T, D + R, dtype=torch.bfloat16, device=DEV)
+    kernels.assemble_rows(torch.from_numpy(chunk_slots).to(DEV), gp["codes"], gp["params"], gp["rope"], gp["hp"],
+                          gp["row_of_slot"], gp["owner_of_row"], None, kc)
+    q = synth.make_normal((T, H, D + R), seed + 1, std=2.0 / (sm * math.sqrt(D + R)))
+    qo = np.zeros(B + 1, np.int32)
+    qo[1:] = np.cumsum(chunks)
+    indptr, indices = index_lists([s[:p] for s, p in zip(slots, prefixes)], pages, page)
+    out = torch.full((T, H, D), float("nan"), dtype=torch.bfloat16, device=DEV)
+    kernels.extend_fwd(q.to(DEV), kc, torch.from_numpy(qo).to(DEV), indptr, indices,
+                       torch.tensor(prefixes, dtype=torch.int64, device=DEV),
+                       torch.tensor(reqs, dtype=torch.int64, device=DEV), gp["codes"], gp["params"], gp["rope"],
+                       gp["hp"], max(chunks), out, sm, P, W, page)
+    torch.cuda.synchronize()
+    kc, out = kc.float().cpu(), out.float().cpu()
+    for b in range(B):
+        s, e, L, pf = qo[b], qo[b + 1], lengths[b], prefixes[b]
+        x = synth.make_latent(L, D, max(1, D // 100), seed=seed * 31 + b)  # the rows build_pool wrote
+        pe = synth.make_normal((L, R), seed * 37 + b)
+        lat32 = codec.rotate(x, rot)[pf:L]
+        assert torch.equal(kc[s:e, :D], attention.chunk_rows(lat32, pf, P, W, "qdq"))
+        assert torch.equal(kc[s:e, D:], pe[pf:L].float())
+        ref, _ = attention.extend(pool, q[s:e, :, :D], q[s:e, :, D:], lat32, pe[pf:L], slots[b][:pf], pf,
+                                  int(reqs[b]), P, W, sm, D, chunk_mode="qdq", dtype=torch.float64)
+        torch.testing.assert_close(out[s:e].double(), ref, rtol=RTOL, atol=ATOL)

@@ -59,7 +59,8 @@ def test_cfg1_writer_serving_shape_flip_rate():
     The rotation runs on bf16 MFMA with FP32 accumulation (exact products, another
     summation order than the oracle's FP32 GEMM), so a code can flip by one level
     where a normalized value sits within rounding of a threshold; the north star
-    allows <= 1e-5 of elements."""
+    allows <= 1e-5 of elements. Measured on this data: 3 of 67,108,864 codes
+    (4.5e-8); the test holds the writer to 5e-7, ten times that."""
     D, R, P, W, page, B, T = 512, 64, 4, 16, 64, 64, 2048
     max_reqs = B + 1
     slots, _, num_slots = alloc_slots([T] * B, page, seed=41)
@@ -95,7 +96,7 @@ def test_cfg1_writer_serving_shape_flip_rate():
     rate = flips / diff.size
     print(f"cfg1 writer: {flips} of {diff.size} codes differ by one level (rate {rate:.2e})")
     assert np.abs(diff).max(initial=0) <= 1
-    assert rate <= 1e-5
+    assert rate <= 5e-7  # the north star's bound is 1e-5
     torch.testing.assert_close(torch.from_numpy(got["params"][loc][..., 0]),
                                torch.from_numpy(ref["params"][loc][..., 0]), rtol=1e-5, atol=0)
     torch.testing.assert_close(torch.from_numpy(got["params"][loc][..., 1]),

@@ -82,3 +82,55 @@ def test_noalloc_rejects_oversized_workspace():
         max_splits, B, H, D, R, 4, 16, 0.1, _p(out), out.stride(0), out.stride(1), _stream(q))
     assert rc == _lib.ROLAQ_ERR_INVALID
     assert "static scratch" in _lib.load().rolaq_last_error().decode()
+
+
+def test_noalloc_captured_replays_equal_decode_fwd():
+    """Captured in a HIP graph after eager calls (its scratch address already
+    looked up), then replayed three times with eager work in between: every
+    replay equals rolaq_decode_fwd bit for bit, and so does a second graph
+    over a smaller batch sharing the same static scratch."""
+    D, R, H, P, W, page = 256, 32, 40, 4, 16, 16
+    sm = 1.0 / math.sqrt(96)
+    lengths = [700, 33, 1500]
+    pool, slots, pages, reqs, _ = build_pool(lengths, D, R, P, W, page, seed=31)
+    gp = pool_to_gpu(pool)
+    q = make_queries(len(lengths), H, D, R, sm, seed=32).to(DEV)
+    max_reqs = len(lengths) + 1
+    for sel, splits, max_splits in (([0, 1, 2], [4, 2, 6], 8), ([2], [3], 4)):
+        qs = q[sel].contiguous()
+        s_slots, s_pages = [slots[i] for i in sel], [pages[i] for i in sel]
+        s_len, s_req = [lengths[i] for i in sel], [reqs[i] for i in sel]
+        out_e, ref = _both(gp, qs, s_slots, s_pages, s_len, s_req, page, splits, max_splits, P, W, sm, max_reqs)
+        assert torch.equal(out_e, ref)
+        indptr, indices = index_lists(s_slots, s_pages, page)
+        seq = torch.tensor(s_len, dtype=torch.int64, device=DEV)
+        req = torch.tensor(np.asarray(s_req), dtype=torch.int64, device=DEV)
+        ns = torch.tensor(splits, dtype=torch.int32, device=DEV)
+        out = torch.full((len(sel), H, D), float("nan"), dtype=torch.bfloat16, device=DEV)
+        graph = torch.cuda.CUDAGraph()
+        stream = torch.cuda.Stream()
+        stream.wait_stream(torch.cuda.current_stream())
+        with torch.cuda.stream(stream), torch.cuda.graph(graph, stream=stream):
+            rc = _noalloc(gp, qs, indptr, indices, page, seq, req, ns, max_splits, P, W, sm, max_reqs, out)
+        _lib.check(rc)
+        for _ in range(3):
+            out.fill_(float("nan"))
+            graph.replay()
+            torch.cuda.synchronize()
+            assert torch.equal(out.cpu(), ref)
+            _ = (qs.float() * 2).sum().item()  # eager work between replays
+
+
+def test_noalloc_first_call_under_capture():
+    """In a fresh process, the entry point's first call (which looks up the
+    static scratch's device address once) made under graph capture: the
+    capture succeeds and its replays equal rolaq_decode_fwd bit for bit
+    (tests/noalloc_capture_child.py, started as a child process)."""
+    import subprocess
+    import sys
+    from pathlib import Path
+
+    child = Path(__file__).resolve().parent / "noalloc_capture_child.py"
+    res = subprocess.run([sys.executable, "-u", str(child)], capture_output=True, text=True, timeout=240)
+    print(res.stdout[-2000:], res.stderr[-2000:])
+    assert res.returncode == 0, res.stdout[-2000:] + res.stderr[-2000:]
