@@ -255,6 +255,7 @@ int decode_args(const char* who, const void* q, int64_t q_stride_b, int64_t q_st
   a->req_idx = req_idx;
   a->num_kv_splits = num_kv_splits;
   a->split_cap = max_kv_splits;
+  a->neutral = 1;
   a->S1 = max_kv_splits + 1;
   a->max_reqs = max_reqs;
   a->B = B;
@@ -308,6 +309,7 @@ int rolaq_decode_fwd(const void* q, int64_t q_stride_b, int64_t q_stride_h, cons
   if (rc != ROLAQ_OK) return rc;
   if (!out) return fail(ROLAQ_ERR_INVALID, "decode_fwd: null pointer");
   a.split_cap = fused_split_cap(B, H, D, max_kv_splits);
+  a.neutral = 0;  // stage 2 merges the quantized splits only
   return hip_status(rolaq_launch_decode(a, D, R, max_kv_splits, static_cast<uint16_t*>(out), out_stride_b,
                                         out_stride_h, kStagePartials | kStageMerge, static_cast<hipStream_t>(stream)),
                     "decode_fwd launch");
@@ -344,6 +346,7 @@ int rolaq_decode_fwd_noalloc(const void* q, int64_t q_stride_b, int64_t q_stride
   if (rc != ROLAQ_OK) return rc;
   if (!out) return fail(ROLAQ_ERR_INVALID, "decode_fwd_noalloc: null pointer");
   a.split_cap = fused_split_cap(B, H, D, max_kv_splits);
+  a.neutral = 0;  // stage 2 merges the quantized splits only
   return hip_status(rolaq_launch_decode(a, D, R, max_kv_splits, static_cast<uint16_t*>(out), out_stride_b,
                                         out_stride_h, kStagePartials | kStageMerge, static_cast<hipStream_t>(stream)),
                     "decode_fwd_noalloc launch");
@@ -380,6 +383,7 @@ int rolaq_decode_merge(const float* attn_logits, const float* attn_lse, const in
   rolaq::DecodeArgs a{};
   a.num_kv_splits = num_kv_splits;
   a.split_cap = max_kv_splits;
+  a.neutral = 1;
   a.S1 = max_kv_splits + 1;
   a.B = B;
   a.H = H;

@@ -46,6 +46,7 @@
 #include "rolaq_common.h"
 #include "rolaq_args.h"
 
+#include <algorithm>
 #include <mutex>
 
 namespace rolaq {
@@ -188,6 +189,14 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
   __shared__ float s_m[kWaves][HG][16];  // per wave: softmax reference of each head
   __shared__ float s_l[kWaves][HG][16];  // per wave: sum of exponentials of each head
 
+  // Every argument the prologue reads, fetched in one batch of scalar loads
+  // (left to itself the compiler issues each where it is first used: one
+  // dependent round trip per use at kernel start).
+  asm volatile("" ::"s"(a.q), "s"(a.q_sb), "s"(a.q_sh), "s"(a.codes), "s"(a.params), "s"(a.rope), "s"(a.hp),
+               "s"(a.kv_indptr), "s"(a.kv_indices), "s"(a.page_shift), "s"(a.seq_lens), "s"(a.req_idx),
+               "s"(a.num_kv_splits), "s"(a.split_cap), "s"(a.S1), "s"(a.max_reqs), "s"(a.H), "s"(a.P),
+               "s"(a.W), "s"(a.sm_scale), "s"(gridDim.x), "s"(gridDim.y));
+
   // ---- which (sequence, head block, split) ------------------------------------
   const int nhb = ((a.H + 15) / 16 + HG - 1) / HG;
   // Head blocks of one (sequence, split) read the same rows: with more than one,
@@ -205,8 +214,14 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
   const int tid = threadIdx.x, lane = tid & 63, la = lane & 15, gq = lane >> 4;
   const int gl = lane_group<D>(gq), s0 = lane_word0<D>(gq);
 
-  // The query loads and the sequence's metadata loads go out together, first
-  // (the tile pipeline waits on both, and on the page lookups that follow).
+  // The sequence's metadata: five loads issued together and waited for once
+  // (the split test below would otherwise wait for its own load first), then
+  // the query's loads, which the first tile needs only after two more round
+  // trips (page lookups, tile data).
+  const int ns_req = a.num_kv_splits[b];
+  const int kv0 = a.kv_indptr[b], kv1 = a.kv_indptr[b + 1];
+  const int64_t req = a.req_idx[b];
+  const int64_t slv = (a.seq_lens ? a.seq_lens : a.req_idx)[b];  // no branch before the loads
   u32x4 qB[HG][KL], qR[HG][KR];
 #pragma unroll
   for (int hg = 0; hg < HG; ++hg) {
@@ -216,15 +231,13 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
 #pragma unroll
     for (int kr = 0; kr < KR; ++kr) qR[hg][kr] = gload<u32x4>(qh + D + 32 * kr + 8 * gq);
   }
-  const int ns = min(a.num_kv_splits[b], a.split_cap);
-  const int kv0 = a.kv_indptr[b], kv1 = a.kv_indptr[b + 1];
-  const int64_t req = a.req_idx[b];
-  const int64_t slv = (a.seq_lens ? a.seq_lens : a.req_idx)[b];  // no branch before the loads
+  asm volatile("" ::"v"(ns_req), "v"(kv0), "v"(kv1), "v"(req), "v"(slv));
+  const int ns = min(ns_req, a.split_cap);
   const int L = a.seq_lens ? (int)slv : kv1 - kv0;
   const int nq = min(max(ns - 1, 1), a.S1 - 1);
   if (split > nq) return;
   if (split == nq) {
-    write_neutral(a, b, h0, nh, split, D);
+    if (a.neutral) write_neutral(a, b, h0, nh, split, D);
     return;
   }
 
@@ -283,6 +296,33 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
     }
   };
 
+  // The window tile's loads (wave 0 of the block holding unit 0) go out in the
+  // prologue: its ring rows with the first page lookups, its rope rows (which
+  // need the pages of their positions) with the first tile's loads.
+  auto win_pos = [&](int i) { return i < n_sink ? i : rec_lo + (i - n_sink); };
+  u32x4 wc[2][KL], wr[2][KR];
+  int32_t wpg[2];
+  auto window_rows = [&]() {
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb) wpg[mb] = page_of(win_pos(min(16 * mb + la, nw - 1)));
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb) {
+      const int pos = win_pos(min(16 * mb + la, nw - 1));
+      const int inner = pos < P ? pos : P + (pos - P) % max(W, 1);
+      const uint16_t* row = a.hp + (1 + req * (P + W) + inner) * D + 128 * gl + 16 * s0;
+#pragma unroll
+      for (int j = 0; j < KL; ++j) wc[mb][j] = gload<u32x4>(row + 16 * (j / 2) + 8 * (j & 1));
+    }
+  };
+  auto window_rope = [&]() {
+#pragma unroll
+    for (int mb = 0; mb < 2; ++mb) {
+      const int pos = win_pos(min(16 * mb + la, nw - 1));
+      const int64_t slot = ((int64_t)wpg[mb] << a.page_shift) + (pos & pmask);
+#pragma unroll
+      for (int kr = 0; kr < KR; ++kr) wr[mb][kr] = gload<u32x4>(a.rope + slot * R + 32 * kr + 8 * gq);
+    }
+  };
   // ---- prologue: the first tile's pages (the query is in flight already), ------
   // the buffer and state set-up while they travel, then the first tile's loads
   TileRegs<D, R> dc, dn;  // the two tile register slots
@@ -292,6 +332,7 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
     lookup(0, pgc);
     lookup(min(1, nl), pgn);
   }
+  if (win_mine) window_rows();
   __builtin_amdgcn_sched_barrier(0);
 
   // while they are in flight: this wave's buffer starts as zeros (see the
@@ -309,6 +350,7 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
   for (int k = 0; k < G::WBUF / 1024; ++k) lds_store128(wbuf + 1024 * k + 16 * lane, u32x4{0u, 0u, 0u, 0u});
   __builtin_amdgcn_sched_barrier(0);
   if (n > 0) load(0, pgc, dn);
+  if (win_mine) window_rope();
   __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
   for (int hg = 0; hg < HG; ++hg) {
@@ -334,21 +376,20 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
   // reference of those heads to its maximum + 8 and scales O and the sum by
   // the difference, in place, before its probabilities are formed. The
   // pending tile's output is already in O (its MFMAs ran inside this tile's
-  // steps). O's lane holds heads 4 gq + j (j = 0..3); their factors come from
-  // the lanes whose row la is that head.
+  // steps). O is held transposed: lane (la, gq) holds head la, the head
+  // whose scores and sum it holds, so its factor is its own.
   auto rescale = [&](const float (&mx)[HG], const uint64_t (&need)[HG]) {
 #pragma unroll
     for (int hg = 0; hg < HG; ++hg) {
-      float fj[4] = {1.f, 1.f, 1.f, 1.f};
+      float f = 1.f;
       if (need[hg]) {
         const float mt = wave_max_over_groups(mx[hg]);
         const float mn = mt > m_ref[hg] + kRefSlack ? mt + kRefHeadroom : m_ref[hg];
-        const float f = __builtin_amdgcn_exp2f(m_ref[hg] - mn);  // 0 when nothing was summed yet
+        f = __builtin_amdgcn_exp2f(m_ref[hg] - mn);  // 0 when nothing was summed yet
         l_lane[hg] *= f;
         m_ref[hg] = mn;
-#pragma unroll
-        for (int j = 0; j < 4; ++j) fj[j] = __shfl(f, 4 * gq + j);
       }
+      const float fj[4] = {f, f, f, f};
 #pragma unroll
       for (int nb = 0; nb < NB; nb += 4)
         scale_acc4(O[hg][nb], O[hg][nb + 1], O[hg][nb + 2], O[hg][nb + 3], fj, need[hg]);
@@ -396,10 +437,13 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
       for (int d = 0; d < 4; ++d) Ph[hg][d] = pack_f16(p[2 * d], p[2 * d + 1]);
     }
   };
+  // O^T[element, head] += V^T P^T: the V^T rows as the A operand, the
+  // probabilities (P[head la][tokens 8 gq + i]) as the B operand, so lane
+  // (la, gq) accumulates head la at elements 16 nb + 4 gq + j
   auto out_nb = [&](int nb, u32x2 v0, u32x2 v1) {
     const u32x4 vt = {v0.x, v0.y, v1.x, v1.y};
 #pragma unroll
-    for (int hg = 0; hg < HG; ++hg) O[hg][nb] = mfma16x16x32_f16(Ph[hg], vt, O[hg][nb]);
+    for (int hg = 0; hg < HG; ++hg) O[hg][nb] = mfma16x16x32_f16(vt, Ph[hg], O[hg][nb]);
   };
   // LDS addresses as a few per-lane bases plus immediate offsets. The swizzle
   // only touches the low 3 bits of a 16-byte chunk index, so
@@ -539,24 +583,8 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
   // score operand's layout, scores them and stores them into its buffer in the
   // expanded layout, where the next tile's steps contract them like an INT2
   // tile (it is always wave 0's first unit: no output is pending before it).
-  auto win_pos = [&](int i) { return i < n_sink ? i : rec_lo + (i - n_sink); };
   auto window_tile = [&](bool first) {
     f32x4 S[2][HG];
-    u32x4 c[2][KL], rp[2][KR];  // both M-blocks' loads in flight together
-    int32_t pg[2];
-#pragma unroll
-    for (int mb = 0; mb < 2; ++mb) pg[mb] = page_of(win_pos(min(16 * mb + la, nw - 1)));
-#pragma unroll
-    for (int mb = 0; mb < 2; ++mb) {
-      const int pos = win_pos(min(16 * mb + la, nw - 1));
-      const int inner = pos < P ? pos : P + (pos - P) % max(W, 1);
-      const uint16_t* row = a.hp + (1 + req * (P + W) + inner) * D + 128 * gl + 16 * s0;
-#pragma unroll
-      for (int j = 0; j < KL; ++j) c[mb][j] = gload<u32x4>(row + 16 * (j / 2) + 8 * (j & 1));
-      const int64_t slot = ((int64_t)pg[mb] << a.page_shift) + (pos & pmask);
-#pragma unroll
-      for (int kr = 0; kr < KR; ++kr) rp[mb][kr] = gload<u32x4>(a.rope + slot * R + 32 * kr + 8 * gq);
-    }
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb) {
       const int i = 16 * mb + la;
@@ -564,13 +592,13 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
       for (int hg = 0; hg < HG; ++hg) S[mb][hg] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int kr = 0; kr < KR; ++kr) {
-        const u32x4 v = i < nw ? rp[mb][kr] : u32x4{0u, 0u, 0u, 0u};
+        const u32x4 v = i < nw ? wr[mb][kr] : u32x4{0u, 0u, 0u, 0u};
 #pragma unroll
         for (int hg = 0; hg < HG; ++hg) S[mb][hg] = mfma16x16x32(v, qR[hg][kr], S[mb][hg]);
       }
 #pragma unroll
       for (int j = 0; j < KL; ++j) {
-        const u32x4 v = i < nw ? bf16x8_to_f16x8(pi_permute(c[mb][j])) : u32x4{0u, 0u, 0u, 0u};
+        const u32x4 v = i < nw ? bf16x8_to_f16x8(pi_permute(wc[mb][j])) : u32x4{0u, 0u, 0u, 0u};
         lds_store128(wb[mb][j & 1] + 128 * (j >> 1), v);  // K-step j of row 16 mb + la
 #pragma unroll
         for (int hg = 0; hg < HG; ++hg) S[mb][hg] = mfma16x16x32_f16(v, qB[hg][j], S[mb][hg]);
@@ -630,88 +658,107 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
       s_l[wave][hg][la] = l_sum[hg];
     }
   }
-  // (no barrier yet: each wave's buffer is its own until the sum below, and
-  // its own reads of it are done, so a wave stores its O as soon as it is
-  // finished while slower waves still run)
-  float* const mbuf = reinterpret_cast<float*>(wbuf);  // this wave's O, [16 heads][D] in LDS element order
+  // Each wave stores its raw O^T (weighted in the sum below) into its own
+  // buffer as head rows of D elements in LDS element order, 16-byte chunk c
+  // of row h at chunk c ^ h (h < 16): the 16 lanes of one lane group write 16
+  // distinct bank groups. No barrier before the stores: each wave's buffer is
+  // its own until the sum, and its own reads of it are done.
+  float* const mbuf = reinterpret_cast<float*>(wbuf);
+  // thread (h, tt) of the sum: head h, octets (K-step j, lane group gq') with
+  // j = tt % KL, gq' = (16 / KL) k + tt / KL; consecutive tt write consecutive
+  // features (an octet of LDS elements is 8 consecutive features in pi order)
+  const int mh = tid >> 4, tt = tid & 15;
 #pragma unroll
   for (int hg = 0; hg < HG; ++hg) {
-    // each wave's raw O (weighted in the sum below, so the accumulators go
-    // to LDS straight from their registers)
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb)
-#pragma unroll
-      for (int r = 0; r < 4; ++r) mbuf[(4 * gq + r) * D + 16 * nb + la] = O[hg][nb][r];
+      *reinterpret_cast<f32x4*>(mbuf + la * D + 4 * ((4 * nb + gq) ^ la)) = O[hg][nb];
     __syncthreads();
-    // sum of the four waves, wave w weighted by exp2(m_w - M) / sum_w' exp2(m_w' - M) l_w';
-    // LDS element 32j + 8gq' + i of a row is feature feature(gq', j, pi(i)),
-    // so 8 consecutive elements are 8 consecutive features in pi order
-    for (int e = tid; e < 16 * D / 8; e += kThreads) {
-      const int h = e / (D / 8), oct = e % (D / 8);
-      const int j = oct / 4, gqo = oct % 4;
-      const int f0 = 128 * lane_group<D>(gqo) + 16 * (lane_word0<D>(gqo) + j / 2) + 8 * (j & 1);
-      float M = kNoRef, Ls = 0.f, wt[kWaves];
+    float M = kNoRef, Ls = 0.f, wt[kWaves];
 #pragma unroll
-      for (int w = 0; w < kWaves; ++w) M = fmaxf(M, s_m[w][hg][h]);
+    for (int w = 0; w < kWaves; ++w) M = fmaxf(M, s_m[w][hg][mh]);
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) {
+      wt[w] = __builtin_amdgcn_exp2f(s_m[w][hg][mh] - M);
+      Ls += wt[w] * s_l[w][hg][mh];
+    }
+    const float inv = Ls > 0.f ? 1.f / Ls : 0.f;
+#pragma unroll
+    for (int w = 0; w < kWaves; ++w) wt[w] *= inv;
+    const int hh = 16 * hg + mh;
+    f32x4 lo4[KL / 4], hi4[KL / 4];
+#pragma unroll
+    for (int k = 0; k < KL / 4; ++k) {
+      const int j = tt % KL, gqo = (16 / KL) * k + tt / KL, oct = 4 * j + gqo;
+      lo4[k] = f32x4{0.f, 0.f, 0.f, 0.f};
+      hi4[k] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int w = 0; w < kWaves; ++w) {
-        wt[w] = __builtin_amdgcn_exp2f(s_m[w][hg][h] - M);
-        Ls += wt[w] * s_l[w][hg][h];
+        const float* src = reinterpret_cast<const float*>(s_buf + w * G::WBUF) + mh * D;
+        lo4[k] += *reinterpret_cast<const f32x4*>(src + 4 * ((2 * oct) ^ mh)) * wt[w];
+        hi4[k] += *reinterpret_cast<const f32x4*>(src + 4 * ((2 * oct + 1) ^ mh)) * wt[w];
       }
-      const float inv = Ls > 0.f ? 1.f / Ls : 0.f;
-      f32x4 lo4 = {0.f, 0.f, 0.f, 0.f}, hi4 = {0.f, 0.f, 0.f, 0.f};
+    }
+    if (hh < nh) {
+      float* const row = a.logits + (((int64_t)b * a.H + h0 + hh) * a.S1 + split) * D;
 #pragma unroll
-      for (int w = 0; w < kWaves; ++w) {
-        const float* src = reinterpret_cast<const float*>(s_buf + w * G::WBUF) + h * D + 8 * oct;
-        const float f = wt[w] * inv;
-        lo4 += *reinterpret_cast<const f32x4*>(src) * f;
-        hi4 += *reinterpret_cast<const f32x4*>(src + 4) * f;
+      for (int k = 0; k < KL / 4; ++k) {
+        const int j = tt % KL, gqo = (16 / KL) * k + tt / KL;
+        const int f0 = 128 * lane_group<D>(gqo) + 16 * (lane_word0<D>(gqo) + j / 2) + 8 * (j & 1);
+        // elements [0..7] of an octet hold features [0, 4, 1, 5, 2, 6, 3, 7]
+        *reinterpret_cast<f32x4*>(row + f0) = f32x4{lo4[k][0], lo4[k][2], hi4[k][0], hi4[k][2]};
+        *reinterpret_cast<f32x4*>(row + f0 + 4) = f32x4{lo4[k][1], lo4[k][3], hi4[k][1], hi4[k][3]};
       }
-      const int hh = 16 * hg + h;
-      if (hh < nh) {
-        float* dst = a.logits + (((int64_t)b * a.H + h0 + hh) * a.S1 + split) * D + f0;
-        // elements [0..7] hold features [0, 4, 1, 5, 2, 6, 3, 7]
-        *reinterpret_cast<f32x4*>(dst) = f32x4{lo4[0], lo4[2], hi4[0], hi4[2]};
-        *reinterpret_cast<f32x4*>(dst + 4) = f32x4{lo4[1], lo4[3], hi4[1], hi4[3]};
-      }
+      if (tt == 0)
+        a.lse[((int64_t)b * a.H + h0 + hh) * a.S1 + split] = Ls > 0.f ? (M + __log2f(Ls)) * kLn2 : kNeutralLse;
     }
-    if (tid < 16 && 16 * hg + tid < nh) {
-      float M = kNoRef, Ls = 0.f;
-      for (int w = 0; w < kWaves; ++w) M = fmaxf(M, s_m[w][hg][tid]);
-      for (int w = 0; w < kWaves; ++w) Ls += __builtin_amdgcn_exp2f(s_m[w][hg][tid] - M) * s_l[w][hg][tid];
-      a.lse[((int64_t)b * a.H + h0 + 16 * hg + tid) * a.S1 + split] =
-          Ls > 0.f ? (M + __log2f(Ls)) * kLn2 : kNeutralLse;
-    }
-    __syncthreads();  // before the next head group reuses the buffers
+    if (hg + 1 < HG) __syncthreads();  // before the next head group reuses the buffers
   }
 }
 
 // ---------------------------------------------------------------------------
-// Stage 2: LSE merge of the nq + 1 partials -> bf16 output.
+// Stage 2: LSE merge of the partials -> bf16 output: the nq quantized splits'
+// partials and, when stage 1 wrote it (neutral = 1), the window split's
+// neutral one. The LSEs and partials of up to kBatch splits are loaded
+// together (one round trip after the split count), then merged online.
 // ---------------------------------------------------------------------------
 template <int D>
 __global__ __launch_bounds__(128) void decode_stage2(const float* __restrict__ logits,
                                                      const float* __restrict__ lse,
                                                      const int32_t* __restrict__ num_kv_splits,
-                                                     int split_cap, int H, int S1, uint16_t* out,
+                                                     int split_cap, int neutral, int H, int S1, uint16_t* out,
                                                      int64_t o_sb, int64_t o_sh) {
   constexpr int FPT = D / 128;
+  constexpr int kBatch = 16;
+  typedef float fv __attribute__((ext_vector_type(FPT)));
   const int b = blockIdx.x / H, h = blockIdx.x % H;
   const int nq = min(max(min(num_kv_splits[b], split_cap) - 1, 1), S1 - 1);
+  const int np = nq + neutral;  // partials to merge (1 <= np <= S1)
   const int64_t row = ((int64_t)b * H + h) * S1;
-  float M = -3.0e38f;
-#pragma unroll 8
-  for (int s = 0; s <= nq; ++s) M = fmaxf(M, lse[row + s]);
-  float acc[FPT], den = 0.f;
+  float M = -3.0e38f, den = 0.f;
+  fv acc = {};
+  for (int s0 = 0; s0 < np; s0 += kBatch) {
+    float ls[kBatch];
+    fv v[kBatch];
 #pragma unroll
-  for (int i = 0; i < FPT; ++i) acc[i] = 0.f;
-#pragma unroll 8
-  for (int s = 0; s <= nq; ++s) {
-    const float w = __builtin_amdgcn_exp2f((lse[row + s] - M) * kLog2e);
-    den += w;
-    const float* src = logits + (row + s) * D + threadIdx.x * FPT;
+    for (int i = 0; i < kBatch; ++i) {
+      const int s = min(s0 + i, np - 1);
+      ls[i] = lse[row + s];
+      v[i] = *reinterpret_cast<const fv*>(logits + (row + s) * D + threadIdx.x * FPT);
+    }
+    float mb = M;
 #pragma unroll
-    for (int i = 0; i < FPT; ++i) acc[i] = fmaf(w, src[i], acc[i]);
+    for (int i = 0; i < kBatch; ++i) mb = s0 + i < np ? fmaxf(mb, ls[i]) : mb;
+    const float c = __builtin_amdgcn_exp2f((M - mb) * kLog2e);  // 0 on the first batch
+    den *= c;
+    acc *= c;
+    M = mb;
+#pragma unroll
+    for (int i = 0; i < kBatch; ++i) {
+      const float w = s0 + i < np ? __builtin_amdgcn_exp2f((ls[i] - M) * kLog2e) : 0.f;
+      den += w;
+      acc += w * v[i];
+    }
   }
   const float inv = 1.f / den;
   uint16_t* dst = out + b * o_sb + h * o_sh + threadIdx.x * FPT;
@@ -741,8 +788,9 @@ hipError_t rolaq_launch_decode(const rolaq::DecodeArgs& a, int D, int R, int max
   const int HG = rolaq_decode_head_groups(D, a.H);
   const int nhb = ((a.H + 15) / 16 + HG - 1) / HG;
   // split rows 0 .. nq, nq = min(max(min(ns, cap) - 1, 1), max_splits): the
-  // quantized splits, then the window split's neutral partial
-  const int rows = a.split_cap < max_splits ? (a.split_cap < 2 ? 2 : a.split_cap) : max_splits + 1;
+  // quantized splits, then (neutral = 1) the window split's neutral partial
+  const int nq_max = std::max(std::min(a.split_cap - 1, max_splits), 1);
+  const int rows = nq_max + (a.neutral ? 1 : 0);
   const dim3 grid(a.B * nhb, rows), block(kThreads);
 #define ROLAQ_S1(DD, RR, GG) \
   if (D == DD && R == RR && HG == GG) hipLaunchKernelGGL((decode_stage1<DD, RR, GG>), grid, block, 0, stream, a);
@@ -757,10 +805,10 @@ hipError_t rolaq_launch_decode(const rolaq::DecodeArgs& a, int D, int R, int max
   if (stages & kStageMerge) {
     if (D == 512)
       hipLaunchKernelGGL((decode_stage2<512>), dim3(a.B * a.H), dim3(128), 0, stream, a.logits, a.lse,
-                         a.num_kv_splits, a.split_cap, a.H, a.S1, out, o_sb, o_sh);
+                         a.num_kv_splits, a.split_cap, a.neutral, a.H, a.S1, out, o_sb, o_sh);
     else if (D == 256)
       hipLaunchKernelGGL((decode_stage2<256>), dim3(a.B * a.H), dim3(128), 0, stream, a.logits, a.lse,
-                         a.num_kv_splits, a.split_cap, a.H, a.S1, out, o_sb, o_sh);
+                         a.num_kv_splits, a.split_cap, a.neutral, a.H, a.S1, out, o_sb, o_sh);
     else
       return hipErrorInvalidValue;
   }

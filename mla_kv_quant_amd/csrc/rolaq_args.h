@@ -19,6 +19,7 @@ struct DecodeArgs {
   const int64_t* req_idx;
   const int32_t* num_kv_splits;
   int split_cap;  // request b uses min(num_kv_splits[b], split_cap) splits
+  int neutral;    // 1: split nq carries the window split's neutral partial; 0: no such partial (fused call)
   int S1;        // max_kv_splits + 1
   int max_reqs;  // requests with ring rows; req_idx outside [0, max_reqs) reads no window rows
   int B, H, P, W;

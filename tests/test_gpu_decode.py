@@ -62,7 +62,8 @@ def run_decode(gp, q, slots, pages, lengths, reqs, page, splits, max_splits, P, 
 def check_against_oracle(pool, q, out, lse, slots, lengths, reqs, splits, P, W, sm_scale, D, max_reqs=None,
                          batch_index=None, max_splits=None):
     """Outputs and merged LSE against the oracle; with ``max_splits`` the
-    partials are those of the fused call (split counts capped)."""
+    partials are those of the fused call (split counts capped, no neutral
+    window-split partial: its slots 0 .. nq - 1 hold every key)."""
     if max_splits is not None:
         splits = fused_splits(splits, q.shape[1], D, max_splits)
     ref, ref_lse = attention.decode(pool, q[..., :D], q[..., D:], slots, lengths, reqs, P, W, sm_scale, D,
@@ -73,7 +74,8 @@ def check_against_oracle(pool, q, out, lse, slots, lengths, reqs, splits, P, W, 
         if lengths[b] == 0:
             continue
         nq = max(splits[b] - 1, 1)
-        merged = torch.logsumexp(lse[b, :, : nq + 1].double(), dim=-1)
+        k = nq if max_splits is not None else nq + 1
+        merged = torch.logsumexp(lse[b, :, :k].double(), dim=-1)
         torch.testing.assert_close(merged, ref_lse[b], rtol=0, atol=2e-3)
 
 
@@ -94,7 +96,7 @@ def test_decode_matches_oracle(case, win):
     out, logits, lse = run_decode(gp, q, slots, pages, lengths, reqs, page, splits, 40, P, W, sm_scale)
     check_against_oracle(pool, q, out, lse, slots, lengths, reqs, splits, P, W, sm_scale, D, max_splits=40)
     for b, ns in enumerate(fused_splits(splits, H, D, 40)):
-        assert torch.isfinite(logits[b, :, : max(ns - 1, 1) + 1]).all()
+        assert torch.isfinite(logits[b, :, : max(ns - 1, 1)]).all()
 
 
 def run_partials(gp, q, slots, pages, lengths, reqs, page, splits, max_splits, P, W, sm_scale):
@@ -179,7 +181,9 @@ def test_packed_mla_decode_entry_and_prepare_splits():
 
 
 def test_partials_then_merge_equals_fused_call():
-    """Stage 1 and stage 2 called apart give the fused call's bytes exactly."""
+    """Stage 1 and stage 2 called apart give the fused call's bytes exactly
+    (the fused call writes no neutral window-split partial; the separate merge
+    gives that partial weight exactly 0)."""
     D, R, H, P, W = 512, 64, 16, 4, 16
     lengths = [5, 300, 1500]
     pool, slots, pages, reqs, _ = build_pool(lengths, D, R, P, W, 64, seed=31)
@@ -202,9 +206,10 @@ def test_partials_then_merge_equals_fused_call():
     kernels.decode_merge(l2, s2, ns, 12, o2)
     torch.cuda.synchronize()
     for b, n in enumerate(splits):
-        k = max(n - 1, 1) + 1
+        k = max(n - 1, 1)
         assert torch.equal(l2[b, :, :k].cpu(), logits[b, :, :k])
         assert torch.equal(s2[b, :, :k].cpu(), lse[b, :, :k])
+        assert (s2[b, :, k] == -1.0e4).all() and (l2[b, :, k] == 0).all()
     assert torch.equal(o2.float().cpu(), out)
 
 
