@@ -47,6 +47,7 @@
 #include "rolaq_args.h"
 
 #include <algorithm>
+#include <type_traits>
 #include <mutex>
 
 namespace rolaq {
@@ -276,7 +277,11 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
   f32x4 O[HG][NB];
   float m_ref[HG], l_lane[HG];
 
-  auto page_of = [&](int pos) { return gload<int32_t>(a.kv_indices + kv0 + (pos >> a.page_shift)); };
+  // page of a position; an empty sequence reads its kv_indptr entry instead
+  // (a valid address; its result is not used)
+  auto page_of = [&](int pos) {
+    return gload<int32_t>(L > 0 ? a.kv_indices + kv0 + (pos >> a.page_shift) : a.kv_indptr + b);
+  };
   auto lookup = [&](int i, int32_t (&pg)[2]) {
     const int base = kTile * (T0 + kWaves * i);
 #pragma unroll
@@ -287,7 +292,8 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb) {
       const int pos = min(base + 16 * mb + la, L - 1);
-      const uint64_t slot = ((uint64_t)(uint32_t)pg[mb] << a.page_shift) + (uint32_t)(pos & pmask);
+      const uint32_t page = L > 0 ? (uint32_t)pg[mb] : 0u;  // empty sequence: slot 0's row, unused
+      const uint64_t slot = ((uint64_t)page << a.page_shift) + (uint32_t)(pos & pmask);
 #pragma unroll
       for (int v = 0; v < CV; ++v) d.code[mb][v] = gload<u32x4>(a.codes + slot * (D / 4) + CB * gq + 16 * v);
       d.prm[mb] = gload<f32x2>(a.params + slot * (2 * NG) + 2 * gl);
@@ -296,15 +302,16 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
     }
   };
 
-  // The window tile's loads (wave 0 of the block holding unit 0) go out in the
-  // prologue: its ring rows with the first page lookups, its rope rows (which
-  // need the pages of their positions) with the first tile's loads.
+  // The window tile's loads (wave 0 of the block holding unit 0), issued in
+  // its prologue.
   auto win_pos = [&](int i) { return i < n_sink ? i : rec_lo + (i - n_sink); };
   u32x4 wc[2][KL], wr[2][KR];
   int32_t wpg[2];
-  auto window_rows = [&]() {
+  auto window_pages = [&]() {
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb) wpg[mb] = page_of(win_pos(min(16 * mb + la, nw - 1)));
+  };
+  auto window_rows = [&]() {
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb) {
       const int pos = win_pos(min(16 * mb + la, nw - 1));
@@ -323,43 +330,10 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
       for (int kr = 0; kr < KR; ++kr) wr[mb][kr] = gload<u32x4>(a.rope + slot * R + 32 * kr + 8 * gq);
     }
   };
-  // ---- prologue: the first tile's pages (the query is in flight already), ------
-  // the buffer and state set-up while they travel, then the first tile's loads
   TileRegs<D, R> dc, dn;  // the two tile register slots
   int32_t pgc[2], pgn[2];  // their pages
-  const int nl = n - 1;
-  if (n > 0) {
-    lookup(0, pgc);
-    lookup(min(1, nl), pgn);
-  }
-  if (win_mine) window_rows();
-  __builtin_amdgcn_sched_barrier(0);
-
-  // while they are in flight: this wave's buffer starts as zeros (see the
-  // pending-output rule below), and the softmax state
+  const int nl = max(n - 1, 0);
   u32x4 Ph[HG];  // the pending tile's probabilities (fp16)
-#pragma unroll
-  for (int hg = 0; hg < HG; ++hg) {
-#pragma unroll
-    for (int nb = 0; nb < NB; ++nb) O[hg][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
-    m_ref[hg] = kNoRef;
-    l_lane[hg] = 0.f;
-    Ph[hg] = u32x4{0u, 0u, 0u, 0u};
-  }
-#pragma unroll
-  for (int k = 0; k < G::WBUF / 1024; ++k) lds_store128(wbuf + 1024 * k + 16 * lane, u32x4{0u, 0u, 0u, 0u});
-  __builtin_amdgcn_sched_barrier(0);
-  if (n > 0) load(0, pgc, dn);
-  if (win_mine) window_rope();
-  __builtin_amdgcn_sched_barrier(0);
-#pragma unroll
-  for (int hg = 0; hg < HG; ++hg) {
-    const bool hv = h0 + 16 * hg + la < a.H;
-#pragma unroll
-    for (int j = 0; j < KL; ++j) qB[hg][j] = hv ? bf16x8_to_f16x8(pi_permute(qB[hg][j])) : u32x4{0u, 0u, 0u, 0u};
-#pragma unroll
-    for (int kr = 0; kr < KR; ++kr) qR[hg][kr] = hv ? qR[hg][kr] : u32x4{0u, 0u, 0u, 0u};
-  }
 
   // The output contraction of a tile runs during the next tile's expansion:
   // word step s of tile i + 1 first reads tile i's V^T for N-blocks 4s..4s+3
@@ -409,7 +383,9 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
   // softmax of one tile's masked scores into Ph; the first tile of a wave sets
   // the reference (nothing is summed yet). One instance per tile, so that O
   // passes through one rescale on every path.
-  auto softmax = [&](const float (&x)[HG][8], bool first) {
+  // (rescaling: std::true_type, or std::false_type for a wave's first unit,
+  // which never rescales, so that O is not touched on that path)
+  auto softmax_impl = [&](const float (&x)[HG][8], bool first, auto rescaling) {
     float mx[HG];
     uint64_t need[HG];  // per head group: lanes past the slack
 #pragma unroll
@@ -423,7 +399,7 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
 #pragma unroll
       for (int hg = 0; hg < HG; ++hg) m_ref[hg] = wave_max_over_groups(mx[hg]) + kRefHeadroom;
     }
-    rescale(mx, need);
+    if constexpr (decltype(rescaling)::value) rescale(mx, need);
 #pragma unroll
     for (int hg = 0; hg < HG; ++hg) {
       float p[8], ls = 0.f;
@@ -437,6 +413,7 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
       for (int d = 0; d < 4; ++d) Ph[hg][d] = pack_f16(p[2 * d], p[2 * d + 1]);
     }
   };
+  auto softmax = [&](const float (&x)[HG][8], bool first) { softmax_impl(x, first, std::true_type{}); };
   // O^T[element, head] += V^T P^T: the V^T rows as the A operand, the
   // probabilities (P[head la][tokens 8 gq + i]) as the B operand, so lane
   // (la, gq) accumulates head la at elements 16 nb + 4 gq + j
@@ -583,22 +560,23 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
   // score operand's layout, scores them and stores them into its buffer in the
   // expanded layout, where the next tile's steps contract them like an INT2
   // tile (it is always wave 0's first unit: no output is pending before it).
-  auto window_tile = [&](bool first) {
+  auto window_tile = [&]() {
     f32x4 S[2][HG];
 #pragma unroll
     for (int mb = 0; mb < 2; ++mb) {
       const int i = 16 * mb + la;
 #pragma unroll
       for (int hg = 0; hg < HG; ++hg) S[mb][hg] = f32x4{0.f, 0.f, 0.f, 0.f};
+      const uint32_t keep = keep_mask(i < nw);  // bit masks, not selects: no branch per K-step
 #pragma unroll
       for (int kr = 0; kr < KR; ++kr) {
-        const u32x4 v = i < nw ? wr[mb][kr] : u32x4{0u, 0u, 0u, 0u};
+        const u32x4 v = wr[mb][kr] & keep;
 #pragma unroll
         for (int hg = 0; hg < HG; ++hg) S[mb][hg] = mfma16x16x32(v, qR[hg][kr], S[mb][hg]);
       }
 #pragma unroll
       for (int j = 0; j < KL; ++j) {
-        const u32x4 v = i < nw ? bf16x8_to_f16x8(pi_permute(wc[mb][j])) : u32x4{0u, 0u, 0u, 0u};
+        const u32x4 v = bf16x8_to_f16x8(pi_permute(wc[mb][j])) & keep;
         lds_store128(wb[mb][j & 1] + 128 * (j >> 1), v);  // K-step j of row 16 mb + la
 #pragma unroll
         for (int hg = 0; hg < HG; ++hg) S[mb][hg] = mfma16x16x32_f16(v, qB[hg][j], S[mb][hg]);
@@ -606,8 +584,75 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
     }
     float x[HG][8];
     masked(S, [&](int tok) { return tok < nw; }, x);
-    softmax(x, first);
+    softmax(x, true);  // always the wave's first unit
   };
+
+  // ---- prologue: the first tiles' pages (the query is in flight already), -----
+  // the buffer, state and query set-up while they travel, then the first
+  // tile's loads. Every wave issues the same loads up to there (a wave with no
+  // tile reads a clamped position's page and row and ignores them): the
+  // compiler's counted waits after a join take the path with the fewest loads
+  // in flight, so a conditional load would make the common code wait for
+  // later loads too. The wave that computes the window tile (wave 0 of the
+  // block holding unit 0) has a prologue of its own: the window's ring rows go
+  // out with the page lookups, its rope rows ahead of the first tile's loads,
+  // and the window tile is computed before the paths join, where the loads
+  // in flight are the same (the first tile's) on both.
+  auto setup = [&]() {
+    // this wave's buffer starts as zeros (see the pending-output rule below),
+    // the softmax state, and the query operands (their loads went out with
+    // the metadata, ahead of the page lookups)
+#pragma unroll
+    for (int hg = 0; hg < HG; ++hg) {
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) O[hg][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+      m_ref[hg] = kNoRef;
+      l_lane[hg] = 0.f;
+      Ph[hg] = u32x4{0u, 0u, 0u, 0u};
+    }
+#pragma unroll
+    for (int k = 0; k < G::WBUF / 1024; ++k) lds_store128(wbuf + 1024 * k + 16 * lane, u32x4{0u, 0u, 0u, 0u});
+#pragma unroll
+    for (int hg = 0; hg < HG; ++hg) {
+      const bool hv = h0 + 16 * hg + la < a.H;
+#pragma unroll
+      for (int j = 0; j < KL; ++j) qB[hg][j] = bf16x8_to_f16x8(pi_permute(qB[hg][j])) & keep_mask(hv);
+#pragma unroll
+      for (int kr = 0; kr < KR; ++kr) qR[hg][kr] &= keep_mask(hv);
+    }
+    // (kept here: left alone, the compiler sinks the conversion to its first
+    // use, past the loads that follow, where it would wait for them)
+#pragma unroll
+    for (int hg = 0; hg < HG; ++hg) {
+#pragma unroll
+      for (int j = 0; j < KL; ++j) asm volatile("" : "+v"(qB[hg][j])::"memory");
+#pragma unroll
+      for (int kr = 0; kr < KR; ++kr) asm volatile("" : "+v"(qR[hg][kr])::"memory");
+    }
+  };
+  bool first = true;
+  if (win_mine) {
+    lookup(0, pgc);
+    lookup(min(1, nl), pgn);
+    window_pages();
+    window_rows();
+    __builtin_amdgcn_sched_barrier(0);
+    setup();
+    __builtin_amdgcn_sched_barrier(0);
+    window_rope();
+    load(0, pgc, dn);
+    __builtin_amdgcn_sched_barrier(0);
+    window_tile();
+    first = false;
+  } else {
+    lookup(0, pgc);
+    lookup(min(1, nl), pgn);
+    __builtin_amdgcn_sched_barrier(0);
+    setup();
+    __builtin_amdgcn_sched_barrier(0);
+    load(0, pgc, dn);
+  }
+  __builtin_amdgcn_sched_barrier(0);
 
   // ---- the wave's units ------------------------------------------------------------
   // Tile pipeline: two register slots (dn, dc) take turns, unrolled by two so
@@ -618,11 +663,6 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
   // one tile of prefetch each. The scheduling barriers keep the issue order,
   // so the compiler's counted waits release tile i while tile i + 1's loads
   // are in flight.
-  bool first = true;
-  if (win_mine) {
-    window_tile(true);
-    first = false;
-  }
   int i = 0;
   for (; i + 1 < n; i += 2) {
     // tile i is in dn: load tile i + 1 into dc, compute tile i

@@ -178,6 +178,9 @@ __device__ __forceinline__ void scale_acc4(f32x4& a, f32x4& b, f32x4& c, f32x4& 
       : "scc");
 }
 
+// all-ones when keep, else zero: a branch-free "keep ? v : 0" on bit patterns
+__device__ __forceinline__ uint32_t keep_mask(bool keep) { return keep ? 0xFFFFFFFFu : 0u; }
+
 __device__ __forceinline__ float wave_max_over_groups(float v) {
   // max over lanes l, l^16, l^32, l^48 (the four 16-lane rows of a wave)
   v = fmaxf(v, __shfl_xor(v, 16));
