@@ -60,6 +60,11 @@ struct ExtGeo {
   static constexpr int KSTR = 2 * DR + 32;          // bytes per key row in LDS (padding measured: +32 B fastest)
   static constexpr int KBYTES = kExtKeys * KSTR;
   static constexpr int BUF = KBYTES;                // one tile: key rows only
+  // tiles per barrier: D = 256 keeps a ring of four tiles in LDS and meets at
+  // a barrier every second tile (fewer points where all eight waves align);
+  // D = 512's tiles allow two buffers, one barrier per tile
+  static constexpr int TPB = D == 256 ? 2 : 1;
+  static constexpr int NBUF = 2 * TPB;
   static constexpr int OPT = D / 256;               // latent octets per loader thread
 };
 
@@ -232,15 +237,24 @@ __global__ __launch_bounds__((64 * ExtGeo<D, R>::WAVES), 1) void extend_kernel(E
     l_run[nb] = 0.f;
   }
 
-  load_keys(0);
-  store_keys(s_buf);
+  constexpr int TPB = G::TPB, NBUF = G::NBUF;
+#pragma unroll
+  for (int t = 0; t < TPB; ++t) {
+    if (t < ntiles) {
+      load_keys(t * kExtKeys);
+      store_keys(s_buf + t * G::BUF);
+    }
+  }
   __syncthreads();
 
+  // Tile it is read from buffer it % NBUF; tile it + TPB is loaded during
+  // tile it and stored after it into the buffer of tile it - TPB, which every
+  // wave finished before the barrier that ended the previous group of TPB tiles.
   for (int it = 0; it < ntiles; ++it) {
-    const uint8_t* kb = s_buf + (it & 1) * G::BUF;
+    const uint8_t* kb = s_buf + (it % NBUF) * G::BUF;
     const int k0 = it * kExtKeys;
-    // loads of the next tile first: they have this tile's compute to land
-    if (it + 1 < ntiles) load_keys(k0 + kExtKeys);
+    // loads of a later tile first: they have this tile's compute to land
+    if (it + TPB < ntiles) load_keys(k0 + TPB * kExtKeys);
 
     // ---- scores S^T[key, row] ----------------------------------------------
     f32x4 s[kExtMK][NBR];
@@ -259,9 +273,20 @@ __global__ __launch_bounds__((64 * ExtGeo<D, R>::WAVES), 1) void extend_kernel(E
     }
 
     // ---- softmax (row = 16 nb + la; keys 16 mk + 4 gq + i) -------------------
-    // A tile that ends before the block's first query position needs no mask
-    // (rows past the last query, qp = -1, stay masked).
+    // Scores stay in raw units (the scale c2 > 0 is applied inside the exp2's
+    // argument, by one FMA). A tile that ends before the block's first query
+    // position needs no causal mask (rows past the last query, qp = -1, stay
+    // masked).
     const bool open = k0 + kExtKeys - 1 <= qfirst;
+#pragma unroll
+    for (int nb = 0; nb < NBR; ++nb) {
+      // key k0 + 16 mk + 4 gq + i is visible to the row when 16 mk + i <= lim
+      const int lim = qp[nb] < 0 ? -1 : (open ? kExtKeys : qp[nb] - k0 - 4 * gq);
+#pragma unroll
+      for (int mk = 0; mk < kExtMK; ++mk)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) s[mk][nb][i] = 16 * mk + i <= lim ? s[mk][nb][i] : kExtMasked;
+    }
     float mx[NBR];
     uint64_t need[NBR];  // lanes whose row passes its reference by more than the slack
 #pragma unroll
@@ -270,12 +295,8 @@ __global__ __launch_bounds__((64 * ExtGeo<D, R>::WAVES), 1) void extend_kernel(E
 #pragma unroll
       for (int mk = 0; mk < kExtMK; ++mk)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int kp = k0 + 16 * mk + 4 * gq + i;
-          const float v = ((open && qp[nb] >= 0) || kp <= qp[nb]) ? s[mk][nb][i] * c2 : kExtMasked;
-          s[mk][nb][i] = v;
-          mx[nb] = fmaxf(mx[nb], v);
-        }
+        for (int i = 0; i < 4; ++i) mx[nb] = fmaxf(mx[nb], s[mk][nb][i]);
+      mx[nb] *= c2;  // log2 units (a masked maximum stays far below any reference)
       need[nb] = __builtin_amdgcn_ballot_w64(it > 0 && mx[nb] > m_ref[nb] + kExtSlack);
     }
     // the first tile sets each row's reference (key 0 is visible to every row)
@@ -312,7 +333,7 @@ __global__ __launch_bounds__((64 * ExtGeo<D, R>::WAVES), 1) void extend_kernel(E
         for (int mk = 0; mk < 2; ++mk)
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
-            p[mk][i] = __builtin_amdgcn_exp2f(s[2 * kh + mk][nb][i] - m_ref[nb]);  // masked: 2^-1e30 = 0
+            p[mk][i] = __builtin_amdgcn_exp2f(fmaf(s[2 * kh + mk][nb][i], c2, -m_ref[nb]));  // masked: 0
             l_run[nb] += p[mk][i];
           }
         pf[kh][nb] = u32x4{pack_f16(p[0][0], p[0][1]), pack_f16(p[0][2], p[0][3]), pack_f16(p[1][0], p[1][1]),
@@ -331,9 +352,9 @@ __global__ __launch_bounds__((64 * ExtGeo<D, R>::WAVES), 1) void extend_kernel(E
         for (int nb = 0; nb < NBR; ++nb) acc_o[nb][nd] = mfma16x16x32_f16(pf[kh][nb], vf, acc_o[nb][nd]);
       }
 
-    // ---- next tile into the other buffer (last read before the previous barrier)
-    if (it + 1 < ntiles) store_keys(s_buf + ((it + 1) & 1) * G::BUF);
-    __syncthreads();
+    // ---- tile it + TPB into the buffer of tile it - TPB ---------------------
+    if (it + TPB < ntiles) store_keys(s_buf + ((it + TPB) % NBUF) * G::BUF);
+    if (it % TPB == TPB - 1 || it + 1 == ntiles) __syncthreads();
   }
 
   // ---- normalise and store -----------------------------------------------------
@@ -363,7 +384,7 @@ hipError_t rolaq_launch_extend(const rolaq::ExtendArgs& a, int D, int R, int max
     using G = ExtGeo<DD, RR>;                                                                           \
     const int64_t rows = (int64_t)max_q_len * a.H;                                                      \
     const dim3 grid((unsigned)a.B, (unsigned)((rows + G::BM - 1) / G::BM));                             \
-    const int lds = 2 * G::BUF;                                                                         \
+    const int lds = G::NBUF * G::BUF;                                                                         \
     const hipError_t e = hipFuncSetAttribute((const void*)extend_kernel<DD, RR>,                        \
                                              hipFuncAttributeMaxDynamicSharedMemorySize, lds);          \
     if (e != hipSuccess) return e;                                                                      \
