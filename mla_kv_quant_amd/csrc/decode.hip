@@ -402,15 +402,14 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
     if constexpr (decltype(rescaling)::value) rescale(mx, need);
 #pragma unroll
     for (int hg = 0; hg < HG; ++hg) {
-      float p[8], ls = 0.f;
+      float p[8];
 #pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        p[i] = __builtin_amdgcn_exp2f(x[hg][i] - m_ref[hg]);  // masked: 2^-1e30 = 0
-        ls += p[i];
-      }
-      l_lane[hg] += ls;
+      for (int i = 0; i < 8; ++i) p[i] = __builtin_amdgcn_exp2f(x[hg][i] - m_ref[hg]);  // masked: 2^-1e30 = 0
 #pragma unroll
       for (int d = 0; d < 4; ++d) Ph[hg][d] = pack_f16(p[2 * d], p[2 * d + 1]);
+      // the sum of the fp16 probabilities the output MFMA uses
+#pragma unroll
+      for (int d = 0; d < 4; ++d) l_lane[hg] = sum_f16x2(Ph[hg][d], l_lane[hg]);
     }
   };
   auto softmax = [&](const float (&x)[HG][8], bool first) { softmax_impl(x, first, std::true_type{}); };

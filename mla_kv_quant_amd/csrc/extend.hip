@@ -334,10 +334,12 @@ __global__ __launch_bounds__((64 * ExtGeo<D, R>::WAVES), 1) void extend_kernel(E
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             p[mk][i] = __builtin_amdgcn_exp2f(fmaf(s[2 * kh + mk][nb][i], c2, -m_ref[nb]));  // masked: 0
-            l_run[nb] += p[mk][i];
           }
         pf[kh][nb] = u32x4{pack_f16(p[0][0], p[0][1]), pack_f16(p[0][2], p[0][3]), pack_f16(p[1][0], p[1][1]),
                            pack_f16(p[1][2], p[1][3])};
+        // the row sum of the fp16 probabilities the output MFMA uses
+#pragma unroll
+        for (int d = 0; d < 4; ++d) l_run[nb] = sum_f16x2(pf[kh][nb][d], l_run[nb]);
       }
 
     // ---- O[row, d] += P . V --------------------------------------------------

@@ -178,6 +178,13 @@ __device__ __forceinline__ void scale_acc4(f32x4& a, f32x4& b, f32x4& c, f32x4& 
       : "scc");
 }
 
+// acc + lo + hi of a packed pair of fp16 values (exact products by one,
+// FP32 accumulation: v_dot2_f32_f16)
+__device__ __forceinline__ float sum_f16x2(uint32_t v, float acc) {
+  typedef _Float16 h2 __attribute__((ext_vector_type(2)));
+  return __builtin_amdgcn_fdot2(__builtin_bit_cast(h2, v), h2{(_Float16)1.0f, (_Float16)1.0f}, acc, false);
+}
+
 // all-ones when keep, else zero: a branch-free "keep ? v : 0" on bit patterns
 __device__ __forceinline__ uint32_t keep_mask(bool keep) { return keep ? 0xFFFFFFFFu : 0u; }
 
