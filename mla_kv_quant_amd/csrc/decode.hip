@@ -479,15 +479,15 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
       t[mb] = make_lut(d.prm[mb], pos >= lo && pos < hi);
     }
     // Word step s: the expansion of step s, the output MFMAs of step s on the
-    // reads issued PFD steps earlier, the stores of step s, its score MFMAs,
-    // then the reads of step s + PFD. Step s stores over the elements its
+    // reads issued PFD steps earlier, the reads of step s + PFD, its score
+    // MFMAs, then the stores of step s. Step s stores over the elements its
     // reads came from; the LDS runs a wave's instructions in order, so those
     // reads (issued earlier) have their data before the stores land, and the
     // only waits are the compiler's, for the read registers. The scheduling
     // groups interleave the output MFMAs with the expansion's VALU work, so
-    // the matrix core runs while the VALU expands, and the score MFMAs with
-    // the next reads. Reads two steps ahead give them a whole step of cover
-    // (one step with three head groups, whose registers are full).
+    // the matrix core runs while the VALU expands. Reads two steps ahead give
+    // them a whole step of cover (one step with three head groups, whose
+    // registers are full).
     constexpr int PFD = HG >= 3 ? 1 : 2;  // steps the transposed reads run ahead
     u32x2 vr[PFD + 1][4][2];
 #pragma unroll
@@ -508,6 +508,12 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
       for (int mb = 0; mb < 2; ++mb) expand_word(d.code[mb][s / 4][s % 4], t[mb], c[mb][0], c[mb][1]);
 #pragma unroll
       for (int k = 0; k < 4; ++k) out_nb(4 * s + k, cur[k][0], cur[k][1]);
+      if (s + PFD < WPL) {
+#pragma unroll
+        for (int k = 0; k < 4; ++k)
+#pragma unroll
+          for (int h = 0; h < 2; ++h) nxt[k][h] = vt_read(4 * (s + PFD) + k, h);
+      }
 #pragma unroll
       for (int mb = 0; mb < 2; ++mb) {
         lds_store128(wb[mb][0] + 128 * s, c[mb][0]);  // K-step 2s
@@ -520,26 +526,20 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
           S[mb][hg] = mfma16x16x32_f16(c[mb][0], qB[hg][2 * s], S[mb][hg]);
           So[mb][hg] = mfma16x16x32_f16(c[mb][1], qB[hg][2 * s + 1], So[mb][hg]);
         }
-      if (s + PFD < WPL) {
-#pragma unroll
-        for (int k = 0; k < 4; ++k)
-#pragma unroll
-          for (int h = 0; h < 2; ++h) nxt[k][h] = vt_read(4 * (s + PFD) + k, h);
-      }
       // issue order: (10 VALU, HG output MFMAs) x 4, the rest of the VALU,
-      // the stores, then (HG score MFMAs, 2 reads) x 4
+      // the transposed reads of step s + PFD, the score MFMAs, the stores
+      // (the reads go out ahead of the stores: the LDS runs a wave's
+      // operations in order, so reads behind 4 KB of stores would wait for
+      // them; their elements are not the ones this step stores)
 #pragma unroll
       for (int k = 0; k < 4; ++k) {
         __builtin_amdgcn_sched_group_barrier(kSchedValu, 10, 0);
         __builtin_amdgcn_sched_group_barrier(kSchedMfma, HG, 0);
       }
       __builtin_amdgcn_sched_group_barrier(kSchedValu, 64, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 8, 0);
+      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 4 * HG, 0);
       __builtin_amdgcn_sched_group_barrier(kSchedDsWrite, 4, 0);
-#pragma unroll
-      for (int k = 0; k < 4; ++k) {
-        __builtin_amdgcn_sched_group_barrier(kSchedMfma, HG, 0);
-        __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 2, 0);
-      }
       __builtin_amdgcn_sched_barrier(0);
     }
     if (HG == 1) {
