@@ -527,7 +527,7 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
           So[mb][hg] = mfma16x16x32_f16(c[mb][1], qB[hg][2 * s + 1], So[mb][hg]);
         }
       // issue order: (10 VALU, HG output MFMAs) x 4, the rest of the VALU,
-      // the transposed reads of step s + PFD, the score MFMAs, the stores
+      // the transposed reads of step s + PFD, then (HG score MFMAs, a store) x 4
       // (the reads go out ahead of the stores: the LDS runs a wave's
       // operations in order, so reads behind 4 KB of stores would wait for
       // them; their elements are not the ones this step stores)
@@ -538,8 +538,11 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
       }
       __builtin_amdgcn_sched_group_barrier(kSchedValu, 64, 0);
       __builtin_amdgcn_sched_group_barrier(kSchedDsRead, 8, 0);
-      __builtin_amdgcn_sched_group_barrier(kSchedMfma, 4 * HG, 0);
-      __builtin_amdgcn_sched_group_barrier(kSchedDsWrite, 4, 0);
+#pragma unroll
+      for (int k = 0; k < 4; ++k) {
+        __builtin_amdgcn_sched_group_barrier(kSchedMfma, HG, 0);
+        __builtin_amdgcn_sched_group_barrier(kSchedDsWrite, 1, 0);
+      }
       __builtin_amdgcn_sched_barrier(0);
     }
     if (HG == 1) {
@@ -699,9 +702,13 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
   }
   // Each wave stores its raw O^T (weighted in the sum below) into its own
   // buffer as head rows of D elements in LDS element order, 16-byte chunk c
-  // of row h at chunk c ^ h (h < 16): the 16 lanes of one lane group write 16
-  // distinct bank groups. No barrier before the stores: each wave's buffer is
-  // its own until the sum, and its own reads of it are done.
+  // of row h at chunk c ^ s(c) ^ h, s(c) = bits 4, 6, 5 of c moved to bits
+  // 0, 1, 2 (only the low 4 bits change, so a chunk stays in its row): the
+  // 16 lanes of one lane group (rows 0..15, one c) write 16 distinct bank
+  // groups, and the 16 threads of one head in the sum read 16 distinct ones.
+  // No barrier before the stores: each wave's buffer is its own until the
+  // sum, and its own reads of it are done.
+  auto mchunk = [](int c, int h) { return c ^ (((c >> 4) & 1) | ((c >> 5) & 2) | ((c >> 3) & 4)) ^ h; };
   float* const mbuf = reinterpret_cast<float*>(wbuf);
   // thread (h, tt) of the sum: head h, octets (K-step j, lane group gq') with
   // j = tt % KL, gq' = (16 / KL) k + tt / KL; consecutive tt write consecutive
@@ -711,7 +718,7 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
   for (int hg = 0; hg < HG; ++hg) {
 #pragma unroll
     for (int nb = 0; nb < NB; ++nb)
-      *reinterpret_cast<f32x4*>(mbuf + la * D + 4 * ((4 * nb + gq) ^ la)) = O[hg][nb];
+      *reinterpret_cast<f32x4*>(mbuf + la * D + 4 * mchunk(4 * nb + gq, la)) = O[hg][nb];
     __syncthreads();
     float M = kNoRef, Ls = 0.f, wt[kWaves];
 #pragma unroll
@@ -725,17 +732,29 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
 #pragma unroll
     for (int w = 0; w < kWaves; ++w) wt[w] *= inv;
     const int hh = 16 * hg + mh;
-    f32x4 lo4[KL / 4], hi4[KL / 4];
+    // every read first (all independent), then the weighted sums
+    f32x4 part[KL / 4][kWaves][2];
+    __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
     for (int k = 0; k < KL / 4; ++k) {
       const int j = tt % KL, gqo = (16 / KL) * k + tt / KL, oct = 4 * j + gqo;
-      lo4[k] = f32x4{0.f, 0.f, 0.f, 0.f};
-      hi4[k] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int w = 0; w < kWaves; ++w) {
         const float* src = reinterpret_cast<const float*>(s_buf + w * G::WBUF) + mh * D;
-        lo4[k] += *reinterpret_cast<const f32x4*>(src + 4 * ((2 * oct) ^ mh)) * wt[w];
-        hi4[k] += *reinterpret_cast<const f32x4*>(src + 4 * ((2 * oct + 1) ^ mh)) * wt[w];
+        part[k][w][0] = *reinterpret_cast<const f32x4*>(src + 4 * mchunk(2 * oct, mh));
+        part[k][w][1] = *reinterpret_cast<const f32x4*>(src + 4 * mchunk(2 * oct + 1, mh));
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    f32x4 lo4[KL / 4], hi4[KL / 4];
+#pragma unroll
+    for (int k = 0; k < KL / 4; ++k) {
+      lo4[k] = part[k][0][0] * wt[0];
+      hi4[k] = part[k][0][1] * wt[0];
+#pragma unroll
+      for (int w = 1; w < kWaves; ++w) {
+        lo4[k] += part[k][w][0] * wt[w];
+        hi4[k] += part[k][w][1] * wt[w];
       }
     }
     if (hh < nh) {
