@@ -33,6 +33,7 @@ import argparse
 import json
 import math
 import os
+import statistics
 import sys
 import time
 from pathlib import Path
@@ -613,12 +614,21 @@ def main():
     # The reference's static 129 (serve.py:198) is timed beside it.
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     ns_best = args.splits if args.splits else -(-cus // db.B) + 1
-    db.alloc_scratch(129)
-    db.set_splits(129)
-    ms129 = time_loop(db.step, max(5, args.steps // 2), args.warmup)
-    db.alloc_scratch(ns_best)
-    db.set_splits(ns_best)
-    ms = time_loop(db.step, args.steps, args.warmup)
+    # the two settings alternate over three rounds (medians), both warmed
+    # first, so that neither carries the other's warm-up or the cold caches
+    # of the first timed loop
+    def at(ns, steps):
+        db.alloc_scratch(ns)
+        db.set_splits(ns)
+        return time_loop(db.step, steps, args.warmup)
+
+    at(129, 1)
+    at(ns_best, 1)
+    r129, rbest = [], []
+    for _ in range(3):
+        r129.append(at(129, max(3, args.steps // 2)))
+        rbest.append(at(ns_best, args.steps))
+    ms129, ms = statistics.median(r129), statistics.median(rbest)
     us_layer = ms * 1000.0 / args.layers
     print(f"[bench] decode: {ns_best} splits {us_layer:.2f} us/layer, the reference's 129 splits "
           f"{ms129 * 1000.0 / args.layers:.2f} us/layer", file=sys.stderr, flush=True)

@@ -2,6 +2,7 @@
 // Validates every argument on the host before any launch; allocates nothing.
 #include <hip/hip_runtime.h>
 
+#include <algorithm>
 #include <cmath>
 #include <cstdarg>
 #include <cstdio>
@@ -280,6 +281,19 @@ int fused_split_cap(int B, int H, int D, int max_kv_splits) {
   return cap < max_kv_splits ? int(cap) : max_kv_splits;
 }
 
+// The fused call's use of its scratch: the capped split count, no neutral
+// window-split partial, and the partials stored at a stride of the capped
+// count rather than max_kv_splits + 1 (attn_logits [B, H, S1c, D] and
+// attn_lse [B, H, S1c] from the start of the buffers, S1c = min(cap - 1,
+// max_kv_splits) + 1 <= max_kv_splits + 1): the partials of one (sequence,
+// head) stay contiguous whatever max_kv_splits is, instead of being spread
+// over a buffer sized for the largest split count.
+void fused_layout(rolaq::DecodeArgs* a, int B, int H, int D, int max_kv_splits) {
+  a->split_cap = fused_split_cap(B, H, D, max_kv_splits);
+  a->neutral = 0;
+  a->S1 = std::max(std::min(a->split_cap - 1, max_kv_splits), 1) + 1;
+}
+
 }  // namespace
 
 extern "C" {
@@ -308,8 +322,7 @@ int rolaq_decode_fwd(const void* q, int64_t q_stride_b, int64_t q_stride_h, cons
                              D, R, P, W, sm_scale, attn_logits, attn_lse, &a);
   if (rc != ROLAQ_OK) return rc;
   if (!out) return fail(ROLAQ_ERR_INVALID, "decode_fwd: null pointer");
-  a.split_cap = fused_split_cap(B, H, D, max_kv_splits);
-  a.neutral = 0;  // stage 2 merges the quantized splits only
+  fused_layout(&a, B, H, D, max_kv_splits);
   return hip_status(rolaq_launch_decode(a, D, R, max_kv_splits, static_cast<uint16_t*>(out), out_stride_b,
                                         out_stride_h, kStagePartials | kStageMerge, static_cast<hipStream_t>(stream)),
                     "decode_fwd launch");
@@ -345,8 +358,7 @@ int rolaq_decode_fwd_noalloc(const void* q, int64_t q_stride_b, int64_t q_stride
                              max_kv_splits, B, H, D, R, P, W, sm_scale, logits, lse, &a);
   if (rc != ROLAQ_OK) return rc;
   if (!out) return fail(ROLAQ_ERR_INVALID, "decode_fwd_noalloc: null pointer");
-  a.split_cap = fused_split_cap(B, H, D, max_kv_splits);
-  a.neutral = 0;  // stage 2 merges the quantized splits only
+  fused_layout(&a, B, H, D, max_kv_splits);
   return hip_status(rolaq_launch_decode(a, D, R, max_kv_splits, static_cast<uint16_t*>(out), out_stride_b,
                                         out_stride_h, kStagePartials | kStageMerge, static_cast<hipStream_t>(stream)),
                     "decode_fwd_noalloc launch");

@@ -141,6 +141,24 @@ def fused_splits(splits, H, D, max_splits):
     return [min(int(ns), cap) for ns in splits]
 
 
+def fused_partials(logits, lse, B, H, D, max_splits):
+    """The split partials a fused rolaq_decode_fwd call left in its scratch,
+    in the standard ``[B, H, max_splits + 1, D]`` / ``[B, H, max_splits + 1]``
+    shape (slots past the fused call's stride are NaN). The fused call stores
+    them from the start of the buffers at a stride of S1c = min(cap - 1,
+    max_splits) + 1 slots per (sequence, head)."""
+    import torch
+    from mla_kv_quant_amd import kernels
+    cap = kernels.decode_split_cap(B, H, D, max_splits)
+    s1c = max(min(cap - 1, max_splits), 1) + 1
+    n = B * H * s1c
+    lg = torch.full((B, H, max_splits + 1, D), float("nan"), dtype=logits.dtype, device=logits.device)
+    ls = torch.full((B, H, max_splits + 1), float("nan"), dtype=lse.dtype, device=lse.device)
+    lg[:, :, :s1c] = logits.reshape(-1)[: n * D].view(B, H, s1c, D)
+    ls[:, :, :s1c] = lse.reshape(-1)[:n].view(B, H, s1c)
+    return lg, ls
+
+
 def rotated_latent(n, D, outliers, seed, rotation):
     """bf16 ``[n, D]`` latent rows in a layer's rotated frame: synthetic rows
     (N(0,1), ``outliers`` channels x20) times ``R_eff = fp32(bf16(R))``, the

@@ -17,8 +17,8 @@ import torch
 from oracle import attention, window
 from mla_kv_quant_amd import kernels, synth
 from mla_kv_quant_amd.decode import packed_mla_decode_gf_fwd, prepare_gf_splits
-from tests.helpers import (alloc_slots, build_pool, fused_splits, gpu_pool_to_oracle, gpu_written_pool,
-                           index_lists, make_queries, pool_to_gpu)
+from tests.helpers import (alloc_slots, build_pool, fused_partials, fused_splits, gpu_pool_to_oracle,
+                           gpu_written_pool, index_lists, make_queries, pool_to_gpu)
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -56,6 +56,7 @@ def run_decode(gp, q, slots, pages, lengths, reqs, page, splits, max_splits, P, 
     kernels.decode_fwd(q.to(DEV), gp["codes"], gp["params"], gp["rope"], gp["hp"], indptr, indices,
                        seq, req, ns, max_splits, logits, lse, out, sm_scale, P, W, page, max_reqs=max_reqs)
     torch.cuda.synchronize()
+    logits, lse = fused_partials(logits, lse, B, H, D, max_splits)
     return out.float().cpu(), logits.cpu(), lse.cpu()
 
 

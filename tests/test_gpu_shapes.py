@@ -18,8 +18,8 @@ import torch
 
 from oracle import attention, layout, window
 from mla_kv_quant_amd import kernels, synth
-from tests.helpers import (alloc_slots, bf16_np_to_torch, fused_splits, gpu_pool_to_oracle, gpu_written_pool,
-                           index_lists, rotated_latent)
+from tests.helpers import (alloc_slots, bf16_np_to_torch, fused_partials, fused_splits, gpu_pool_to_oracle,
+                           gpu_written_pool, index_lists, rotated_latent)
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -40,7 +40,8 @@ def _decode(gp, q, slots, pages, lengths, reqs, page, splits, max_splits, P, W, 
                        torch.tensor(splits, dtype=torch.int32, device=DEV), max_splits, logits, lse, out, sm, P, W,
                        page)
     torch.cuda.synchronize()
-    # the split counts the fused call used (its partials' layout)
+    # the split counts the fused call used, and its partials in the standard shape
+    _, lse = fused_partials(logits, lse, B, H, D, max_splits)
     return out.float().cpu(), lse.cpu(), fused_splits(splits, H, D, max_splits)
 
 
