@@ -139,11 +139,14 @@ int rolaq_prepare_gf_splits(const int32_t* splits, int32_t* quant, int32_t* merg
  * add partials to write and merge, and SGLang reads only the merged output;
  * the output does not depend on the split count beyond FP32 summation order).
  * Positions P <= t < L_b - W and the window rows are split over
- * max(ns'_b - 1, 1) splits (the window rows go with split 0); split
- * max(ns'_b - 1, 1), the reference's window split, holds the neutral partial.
- * Partials (normalised output, natural-log LSE; empty splits 0 / -1e4) go to
- * attn_logits fp32 [B, H, max_kv_splits + 1, D] (16-byte aligned) and
- * attn_lse fp32 [B, H, max_kv_splits + 1]; the merged output to out: bf16
+ * nq_b = max(ns'_b - 1, 1) splits (the window rows go with split 0); the
+ * reference's separate window split has no partial of its own here.
+ * attn_logits (fp32, 16-byte aligned, at least B * H * (max_kv_splits + 1) * D
+ * floats) and attn_lse (fp32, at least B * H * (max_kv_splits + 1)) are
+ * scratch: the call uses their first B * H * S1c * D and B * H * S1c floats as
+ * [B, H, S1c, D] and [B, H, S1c], S1c = min(cap - 1, max_kv_splits) + 1, and
+ * writes partials (normalised output, natural-log LSE; empty splits 0 / -1e4)
+ * to slots 0 .. nq_b - 1 of each (b, h). The merged output goes to out: bf16
  * [B, H, D] with strides (out_stride_b, out_stride_h), in the rotated frame.
  * Supported shapes: (D, R) = (512, 64) or (256, 32), 1 <= H <= 128; window
  * P + W <= 32. Latent values (query, stored levels, window rows) are carried
