@@ -65,12 +65,16 @@ __global__ __launch_bounds__(256) void pack_rows_kernel(const T* __restrict__ x,
 #pragma unroll
   for (int o = 1; o < 16; o <<= 1) q += __shfl_xor(q, o);
   const float std_ = sqrtf(q * (1.0f / 128.0f) + 1e-08f);
-  const float rstd = 1.0f / std_;
+  // code = #{-t, 0, t <= (x - mean) / std} (correctly rounded quotient,
+  // oscar.py:135-140), compared through the row's thresholds on x - mean
+  const double sd = (double)std_;
+  const float ylo = y_threshold(sd, below_midpoint(-thr), threshold_inclusive(-thr));
+  const float y0 = y_threshold(sd, below_midpoint(0.0f), true);
+  const float yhi = y_threshold(sd, below_midpoint(thr), threshold_inclusive(thr));
   uint32_t bits = 0;
 #pragma unroll
   for (int i = 0; i < 8; ++i) {
-    const float nrm = div_by(v[i], std_, rstd);  // correctly rounded, as oscar.py:135 divides
-    const uint32_t c = uint32_t(nrm >= -thr) + uint32_t(nrm >= 0.f) + uint32_t(nrm >= thr);
+    const uint32_t c = uint32_t(v[i] >= ylo) + uint32_t(v[i] >= y0) + uint32_t(v[i] >= yhi);
     bits |= c << (2 * i);
   }
   // elements 8l .. 8l+7 of the row: bytes 2l, 2l+1 (element j at byte j/4, bits 2(j%4))

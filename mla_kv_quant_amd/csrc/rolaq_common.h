@@ -55,14 +55,31 @@ __device__ __forceinline__ uint16_t float_to_bf16(float f) {
   return uint16_t(pack_bf16(f, 0.0f) & 0xffffu);
 }
 
-// The correctly rounded FP32 quotient d / s from y = RN(1 / s) (one true
-// division per divisor): q0 = RN(d y), the exact remainder r = d - q0 s, then
-// RN(q0 + r y) (Markstein's quotient correction with a fused multiply-add,
-// P. Markstein, IBM J. Res. Dev. 34(1), 1990). Used where many values share a
-// divisor; checked against true division in tests/test_division_identity.py.
-__device__ __forceinline__ float div_by(float d, float s, float y) {
-  const float q0 = d * y;
-  return fmaf(fmaf(-q0, s, d), y, q0);
+// Lloyd code thresholds moved from the quotient to its numerator. For a float
+// threshold th and s > 0, RN(y / s) >= th holds exactly when y / s >= mu, or
+// y / s > mu when th's significand is odd (the tie at mu then rounds to the
+// float below th), mu being the midpoint of th and the next float below it.
+// mu has at most 26 significant bits, so s * mu is exact in FP64, and the
+// smallest float y passing the test is s * mu rounded up (one float further
+// when the test is strict and s * mu is itself a float). Comparing y with
+// these per-row floats gives the codes of the correctly rounded quotient
+// (mla_quant/oscar.py:135-140) with no division per element; checked against
+// true division in tests/test_division_identity.py.
+__device__ __forceinline__ double below_midpoint(float th) {
+  const uint32_t b = __float_as_uint(th);
+  const uint32_t below = (b << 1) == 0 ? 0x80000001u : ((int32_t)b < 0 ? b + 1 : b - 1);
+  return 0.5 * ((double)__uint_as_float(below) + (double)th);
+}
+
+__device__ __forceinline__ bool threshold_inclusive(float th) { return (__float_as_uint(th) & 1u) == 0; }
+
+__device__ __forceinline__ float y_threshold(double s, double mu, bool incl) {
+  const double p = s * mu;
+  const float y = (float)p;
+  const double yd = (double)y;
+  if (incl ? !(yd < p) : !(yd <= p)) return y;  // also NaN: every test fails
+  const uint32_t b = __float_as_uint(y);
+  return __uint_as_float((b << 1) == 0 ? 1u : ((int32_t)b < 0 ? b - 1 : b + 1));
 }
 
 // Load through a global (address space 1) pointer: a global_load, which only

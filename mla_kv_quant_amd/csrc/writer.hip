@@ -82,6 +82,14 @@ __device__ __forceinline__ u32x4 rms_apply8(u32x4 v, float r, u32x4 gm) {
 }
 
 
+// 2 w + (this lane's bit of the lane mask m): one add with carry-in.
+__device__ __forceinline__ uint32_t twice_plus_bit(uint32_t w, uint64_t m) {
+  uint32_t r;
+  uint64_t carry_out;
+  asm("v_addc_co_u32_e64 %0, %1, %2, %2, %3" : "=v"(r), "=s"(carry_out) : "v"(w), "s"(m));
+  return r;
+}
+
 // A field of the kernel's WriterArgs argument, loaded from the kernel argument
 // segment where it is used. This relies on WriterArgs being writer_kernel's only
 // explicit argument (so it sits at offset 0 of the segment) with the host's
@@ -247,35 +255,86 @@ __global__ __launch_bounds__(64 * kWriterWaves, 1) void writer_kernel(WriterArgs
     for (int mb = 0; mb < 8; ++mb)
 #pragma unroll
       for (int nb = 0; nb < 4; ++nb) acc[mb][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int ks = 0; ks < KS; ++ks) {
-      const int cur = ks % kWriterDepth;
-      u32x4 av[8], xv[4];
-#pragma unroll
-      for (int mb = 0; mb < 8; ++mb) av[mb] = *reinterpret_cast<const u32x4*>(lds_a + 16 * mb * STR + 64 * ks);
+    // K-step k's latent slice (normalized under NORM) is moved to the MFMA
+    // layout by stage(k), which then reuses its ring slot for the load
+    // kWriterDepth steps further on. Under NORM the K loop is software
+    // pipelined: stage(k) and the first half of step k's R_g rows are issued
+    // between the two halves of step k - 1's MFMAs, the second half of its
+    // R_g rows before its own first half.
+    u32x4 xv[2][4], av[2][8];
+    auto stage = [&](int k) {
+      const int s = k % kWriterDepth;
       if constexpr (NORM) {
-        const u32x4 gm = *reinterpret_cast<const u32x4*>(s_gamma + 64 * ks + 16 * (lane & 3));
+        const u32x4 gm = *reinterpret_cast<const u32x4*>(s_gamma + 64 * k + 16 * (lane & 3));
 #pragma unroll
         for (int nb = 0; nb < 4; ++nb) {
-          xb[cur][nb] = rms_apply8(xb[cur][nb], rinv[nb], gm);
-          if (ystore && ks % NG == g)  // rows at or past n fall outside the buffer and are dropped
+          xb[s][nb] = rms_apply8(xb[s][nb], rinv[nb], gm);
+          if (ystore && k % NG == g)  // rows at or past n fall outside the buffer and are dropped
             __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(__attribute__((ext_vector_type(4))) uint32_t,
-                                                                      xb[cur][nb]),
-                                                   ys_rsrc, yoff + 64 * ks, nb * 16 * yrow, 0);
+                                                                      xb[s][nb]),
+                                                   ys_rsrc, yoff + 64 * k, nb * 16 * yrow, 0);
         }
       }
 #pragma unroll
-      for (int nb = 0; nb < 4; ++nb) xv[nb] = relayout(xb[cur][nb]);
-      const int kk = ks + kWriterDepth;
+      for (int nb = 0; nb < 4; ++nb) xv[k % 2][nb] = relayout(xb[s][nb]);
+      const int kk = k + kWriterDepth;
 #pragma unroll
-      for (int nb = 0; nb < 4; ++nb) xb[cur][nb] = kk < KS ? xload(rs, nb, kk) : xload(rn, nb, kk - KS);
+      for (int nb = 0; nb < 4; ++nb) xb[s][nb] = kk < KS ? xload(rs, nb, kk) : xload(rn, nb, kk - KS);
+    };
+    auto rread = [&](int k, int m0) {
 #pragma unroll
-      for (int mb = 0; mb < 8; ++mb)
+      for (int mb = m0; mb < m0 + 4; ++mb)
+        av[k % 2][mb] = *reinterpret_cast<const u32x4*>(lds_a + 16 * mb * STR + 64 * k);
+    };
+    if constexpr (NORM) {
+      stage(0);
+      rread(0, 0);
 #pragma unroll
-        for (int nb = 0; nb < 4; ++nb) acc[mb][nb] = mfma16x16x32(av[mb], xv[nb], acc[mb][nb]);
-      // one K-step per scheduling region: hoisting every step's LDS reads
-      // ahead of the unrolled loop would exhaust the registers
-      __builtin_amdgcn_sched_barrier(0);
+      for (int ks = 0; ks < KS; ++ks) {
+        const int c = ks % 2;
+        rread(ks, 4);
+#pragma unroll
+        for (int mb = 0; mb < 4; ++mb)
+#pragma unroll
+          for (int nb = 0; nb < 4; ++nb) acc[mb][nb] = mfma16x16x32(av[c][mb], xv[c][nb], acc[mb][nb]);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          __builtin_amdgcn_sched_group_barrier(0x080, 1, 0);  // an LDS read
+          __builtin_amdgcn_sched_group_barrier(0x008, 4, 0);  // four MFMAs
+        }
+        __builtin_amdgcn_sched_barrier(0);
+        if (ks + 1 < KS) {
+          stage(ks + 1);
+          rread(ks + 1, 0);
+        }
+#pragma unroll
+        for (int mb = 4; mb < 8; ++mb)
+#pragma unroll
+          for (int nb = 0; nb < 4; ++nb) acc[mb][nb] = mfma16x16x32(av[c][mb], xv[c][nb], acc[mb][nb]);
+        if (ks + 1 < KS) {
+#pragma unroll
+          for (int i = 0; i < 16; ++i) {
+            __builtin_amdgcn_sched_group_barrier(0x080, 1, 0);  // a relayout permute or LDS read
+            __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);  // an MFMA
+          }
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    } else {
+      // without the norm the staged operands' registers are worth more than
+      // the overlap (measured): one K-step per scheduling region
+#pragma unroll
+      for (int ks = 0; ks < KS; ++ks) {
+        const int c = ks % 2;
+        rread(ks, 0);
+        rread(ks, 4);
+        stage(ks);
+#pragma unroll
+        for (int mb = 0; mb < 8; ++mb)
+#pragma unroll
+          for (int nb = 0; nb < 4; ++nb) acc[mb][nb] = mfma16x16x32(av[c][mb], xv[c][nb], acc[mb][nb]);
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
 
     // ---- epilogue: lane (la, gq) holds columns 32gq..32gq+31 of row 16nb+la ---
@@ -285,6 +344,10 @@ __global__ __launch_bounds__(64 * kWriterWaves, 1) void writer_kernel(WriterArgs
     int lane_now;
     asm volatile("v_mbcnt_lo_u32_b32 %0, -1, 0\n\tv_mbcnt_hi_u32_b32 %0, -1, %0" : "=v"(lane_now));
     const int lr = lane_now & 15, gr = lane_now >> 4;
+    // the code thresholds -t, 0, t as midpoints (FP64) and tie rules
+    const float thr = a.thr;
+    const double mu_lo = below_midpoint(-thr), mu_hi = below_midpoint(thr), mu_zero = below_midpoint(0.0f);
+    const bool incl_lo = threshold_inclusive(-thr), incl_hi = threshold_inclusive(thr);
     int64_t slot[4];
     int32_t seq[4], pos[4], req[4];
     u32x2 pes[4];
@@ -342,17 +405,21 @@ __global__ __launch_bounds__(64 * kWriterWaves, 1) void writer_kernel(WriterArgs
       q = sum_over_rows(q);
       const float std_ = sqrtf(q * (1.0f / 128.0f) + 1e-08f);
       // code = #{-t, 0, t <= normalized}, normalized = (x - mean) / std, the
-      // correctly rounded FP32 quotient (oscar.py:135-140, operation for operation)
-      const float t = a.thr;
-      const float rstd = 1.0f / std_;
+      // correctly rounded FP32 quotient (oscar.py:135-140): compared through
+      // the row's exact thresholds on y = x - mean (no division per element).
+      // Its two bits: high = (y >= y0), low = the parity of the three tests.
+      const double sd = (double)std_;
+      const float ylo = y_threshold(sd, mu_lo, incl_lo), y0 = y_threshold(sd, mu_zero, true),
+                  yhi = y_threshold(sd, mu_hi, incl_hi);
       uint32_t word[2] = {0u, 0u};
 #pragma unroll
-      for (int mb = 0; mb < 8; ++mb)
+      for (int wi = 0; wi < 2; ++wi)
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float nrm = div_by(acc[mb][nb][i], std_, rstd);
-          const uint32_t c = uint32_t(nrm >= -t) + uint32_t(nrm >= 0.f) + uint32_t(nrm >= t);
-          word[mb >> 2] |= c << (2 * (4 * (mb & 3) + i));
+        for (int e = 15; e >= 0; --e) {  // Horner, element e at bits 2e, 2e + 1
+          const float y = acc[4 * wi + e / 4][nb][e % 4];
+          const uint64_t hi = __builtin_amdgcn_ballot_w64(y >= y0);
+          const uint64_t lo = __builtin_amdgcn_ballot_w64(y >= ylo) ^ hi ^ __builtin_amdgcn_ballot_w64(y >= yhi);
+          word[wi] = twice_plus_bit(twice_plus_bit(word[wi], hi), lo);
         }
       if (live) {
         // words 2gq, 2gq+1 of group g: row words 8g + 2gq, 8g + 2gq + 1
