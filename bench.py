@@ -413,21 +413,22 @@ def cpu_baseline(db: "DecodeBench", dev: str):
     med, ts = _median_runs(lambda: codec.rotate_quantize(x0, rot))
     legs["cfg0_codec_qdq"] = {"value": round(med * 1e3, 2), "unit": "ms", "rows": 4096,
                               "runs_s": [round(t, 4) for t in ts]}
-    # cfg1: one layer = FP32 rotation GEMM + QDQ of 131072 rows; sample 16384 rows, scaled x8
-    x1 = synth.make_latent(16384, 512, 5, seed=91)
+    # cfg1: one layer = FP32 rotation GEMM + QDQ of all 131072 rows
+    x1 = synth.make_latent(131072, 512, 5, seed=91)
     med, ts = _median_runs(lambda: codec.rotate_quantize(x1, rot))
-    legs["cfg1_rotate_qdq_layer"] = {"value": round(med * 8 * 1e3, 1), "unit": "ms/layer",
-                                     "sample": "16384 of 131072 rows, scaled x8", "runs_s": [round(t, 4) for t in ts]}
-    # cfg2 / cfg4a: one layer of dequantize-then-attention
-    legs["cfg2_attention_layer"] = _attention_leg(db, 2, 32)
-    db4 = DecodeBench(1, dev, B=2, lengths=[16384] * 2, H=40, D=256, R=32, seed=4)
-    legs["cfg4a_attention_layer"] = _attention_leg(db4, 2, 64)
+    legs["cfg1_rotate_qdq_layer"] = {"value": round(med * 1e3, 1), "unit": "ms/layer",
+                                     "sample": "all 131072 rows of one layer", "runs_s": [round(t, 4) for t in ts]}
+    # cfg2 / cfg4a: one layer of dequantize-then-attention (cfg2 whole, cfg4a a quarter of the batch)
+    legs["cfg2_attention_layer"] = _attention_leg(db, db.B, db.B)
+    db4 = DecodeBench(1, dev, B=16, lengths=[16384] * 16, H=40, D=256, R=32, seed=4)
+    legs["cfg4a_attention_layer"] = _attention_leg(db4, 16, 64)
     del db4
     torch.cuda.empty_cache()
     head = legs["cfg2_attention_layer"]
     return {"value": head["value"], "unit": "us/layer", "cores": threads, "kind": "port",
-            "sample": "cfg2 leg: oracle dequantize-then-attention (torch CPU, FP32) on 2 of the 32 sequences x 16384 "
-                      "tokens of one layer, median of 5 runs, scaled x16 to one layer",
+            "sample": f"cfg2 leg: oracle dequantize-then-attention (torch CPU, FP32) over all {db.B} sequences x "
+                      f"{db.L} tokens of one layer, median of 5 runs after one warm-up (about 10 s of CPU work "
+                      f"with the other legs)",
             "nproc": threads, "cpu_model": _cpu_model(), "legs": legs}
 
 
