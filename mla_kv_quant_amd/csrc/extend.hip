@@ -262,13 +262,26 @@ __global__ __launch_bounds__((64 * ExtGeo<D, R>::WAVES), 1) void extend_kernel(E
     for (int mk = 0; mk < kExtMK; ++mk)
 #pragma unroll
       for (int nb = 0; nb < NBR; ++nb) s[mk][nb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    // the K operands of K-step ks + 1 are read while step ks's MFMAs run
+    auto kread = [&](int ks, int mk) {
+      return *reinterpret_cast<const u32x4*>(kb + (16 * mk + la) * G::KSTR + 64 * ks + 16 * gq);
+    };
+    u32x4 kf[2][kExtMK];
+#pragma unroll
+    for (int mk = 0; mk < kExtMK; ++mk) kf[0][mk] = kread(0, mk);
 #pragma unroll
     for (int ks = 0; ks < KSQ; ++ks) {
+      if (ks + 1 < KSQ) {
 #pragma unroll
-      for (int mk = 0; mk < kExtMK; ++mk) {
-        const u32x4 kf = *reinterpret_cast<const u32x4*>(kb + (16 * mk + la) * G::KSTR + 64 * ks + 16 * gq);
+        for (int mk = 0; mk < kExtMK; ++mk) kf[(ks + 1) & 1][mk] = kread(ks + 1, mk);
+      }
 #pragma unroll
-        for (int nb = 0; nb < NBR; ++nb) s[mk][nb] = mfma16x16x32_f16(kf, qf[nb][ks], s[mk][nb]);
+      for (int mk = 0; mk < kExtMK; ++mk)
+#pragma unroll
+        for (int nb = 0; nb < NBR; ++nb) s[mk][nb] = mfma16x16x32_f16(kf[ks & 1][mk], qf[nb][ks], s[mk][nb]);
+      if (ks + 1 < KSQ) {
+        __builtin_amdgcn_sched_group_barrier(0x100, kExtMK, 0);  // the next step's reads
+        __builtin_amdgcn_sched_group_barrier(0x008, kExtMK * NBR, 0);
       }
     }
 
