@@ -427,7 +427,7 @@ def cpu_baseline(db: "DecodeBench", dev: str):
     head = legs["cfg2_attention_layer"]
     return {"value": head["value"], "unit": "us/layer", "cores": threads, "kind": "port",
             "sample": f"cfg2 leg: oracle dequantize-then-attention (torch CPU, FP32) over all {db.B} sequences x "
-                      f"{db.L} tokens of one layer, median of 5 runs after one warm-up (about 10 s of CPU work "
+                      f"{db.L} tokens of one layer, median of 5 runs after one warm-up (about 8 s of CPU work "
                       f"with the other legs)",
             "nproc": threads, "cpu_model": _cpu_model(), "legs": legs}
 
