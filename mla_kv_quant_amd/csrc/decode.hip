@@ -364,9 +364,10 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
         m_ref[hg] = mn;
       }
       const float fj[4] = {f, f, f, f};
+      static_assert(NB % 16 == 0, "rescale in groups of 16 N-blocks");
 #pragma unroll
-      for (int nb = 0; nb < NB; nb += 4)
-        scale_acc4(O[hg][nb], O[hg][nb + 1], O[hg][nb + 2], O[hg][nb + 3], fj, need[hg]);
+      for (int nb = 0; nb < NB; nb += 16)
+        scale_acc16(*reinterpret_cast<f32x4(*)[16]>(&O[hg][nb]), fj, need[hg]);
     }
   };
   // the scores of one tile in log2 units, masked by the validity of token

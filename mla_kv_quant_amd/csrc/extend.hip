@@ -27,7 +27,7 @@
 //   softmax in the log2 domain against a per-row reference (the row's maximum
 //   over the first tile + 8); a tile whose scores pass it by more than 15
 //   moves it to the tile's maximum + 8 and scales O and the row sum by the
-//   difference in place (scale_acc4), so every probability fits fp16
+//   difference in place (scale_acc16), so every probability fits fp16
 //   O[RW rows, D] += P . V           on fp16 MFMA 16x16x32 per 32-key half, the keys of
 //                                     each lane taken in the order the score MFMA left
 //                                     them, P rounded to fp16 (relative error 2^-12).
@@ -332,9 +332,10 @@ __global__ __launch_bounds__((64 * ExtGeo<D, R>::WAVES), 1) void extend_kernel(E
 #pragma unroll
         for (int i = 0; i < 4; ++i) fj[i] = __shfl(f, 4 * gq + i);
       }
+      static_assert(ND % 16 == 0, "rescale in groups of 16 column blocks");
 #pragma unroll
-      for (int nd = 0; nd < ND; nd += 4)
-        scale_acc4(acc_o[nb][nd], acc_o[nb][nd + 1], acc_o[nb][nd + 2], acc_o[nb][nd + 3], fj, need[nb]);
+      for (int nd = 0; nd < ND; nd += 16)
+        scale_acc16(*reinterpret_cast<f32x4(*)[16]>(&acc_o[nb][nd]), fj, need[nb]);
     }
     u32x4 pf[kExtKH][NBR];
 #pragma unroll

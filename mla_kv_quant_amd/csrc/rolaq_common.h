@@ -195,6 +195,39 @@ __device__ __forceinline__ void scale_acc4(f32x4& a, f32x4& b, f32x4& c, f32x4& 
       : "scc");
 }
 
+// scale_acc4 over 16 accumulator tuples behind one test of the lane mask
+// (one branch instead of four when nothing is scaled)
+__device__ __forceinline__ void scale_acc16(f32x4 (&o)[16], const float (&f)[4], uint64_t need) {
+  float t0, t1, t2, t3;
+  asm volatile(
+      "s_cmp_lg_u64 %24, 0\n\t"
+      "s_cbranch_scc0 1f\n\t"
+      "s_nop 7\n\ts_nop 7\n\t"
+      "ROLAQ_ACC_SCALE %0, %16, %17, %18, %19, %20, %21, %22, %23\n\t"
+      "ROLAQ_ACC_SCALE %1, %16, %17, %18, %19, %20, %21, %22, %23\n\t"
+      "ROLAQ_ACC_SCALE %2, %16, %17, %18, %19, %20, %21, %22, %23\n\t"
+      "ROLAQ_ACC_SCALE %3, %16, %17, %18, %19, %20, %21, %22, %23\n\t"
+      "ROLAQ_ACC_SCALE %4, %16, %17, %18, %19, %20, %21, %22, %23\n\t"
+      "ROLAQ_ACC_SCALE %5, %16, %17, %18, %19, %20, %21, %22, %23\n\t"
+      "ROLAQ_ACC_SCALE %6, %16, %17, %18, %19, %20, %21, %22, %23\n\t"
+      "ROLAQ_ACC_SCALE %7, %16, %17, %18, %19, %20, %21, %22, %23\n\t"
+      "ROLAQ_ACC_SCALE %8, %16, %17, %18, %19, %20, %21, %22, %23\n\t"
+      "ROLAQ_ACC_SCALE %9, %16, %17, %18, %19, %20, %21, %22, %23\n\t"
+      "ROLAQ_ACC_SCALE %10, %16, %17, %18, %19, %20, %21, %22, %23\n\t"
+      "ROLAQ_ACC_SCALE %11, %16, %17, %18, %19, %20, %21, %22, %23\n\t"
+      "ROLAQ_ACC_SCALE %12, %16, %17, %18, %19, %20, %21, %22, %23\n\t"
+      "ROLAQ_ACC_SCALE %13, %16, %17, %18, %19, %20, %21, %22, %23\n\t"
+      "ROLAQ_ACC_SCALE %14, %16, %17, %18, %19, %20, %21, %22, %23\n\t"
+      "ROLAQ_ACC_SCALE %15, %16, %17, %18, %19, %20, %21, %22, %23\n\t"
+      "s_nop 7\n"
+      "1:"
+      : "+a"(o[0]), "+a"(o[1]), "+a"(o[2]), "+a"(o[3]), "+a"(o[4]), "+a"(o[5]), "+a"(o[6]), "+a"(o[7]),
+        "+a"(o[8]), "+a"(o[9]), "+a"(o[10]), "+a"(o[11]), "+a"(o[12]), "+a"(o[13]), "+a"(o[14]), "+a"(o[15]),
+        "=&v"(t0), "=&v"(t1), "=&v"(t2), "=&v"(t3)
+      : "v"(f[0]), "v"(f[1]), "v"(f[2]), "v"(f[3]), "s"(need)
+      : "scc");
+}
+
 // acc + lo + hi of a packed pair of fp16 values (exact products by one,
 // FP32 accumulation: v_dot2_f32_f16)
 __device__ __forceinline__ float sum_f16x2(uint32_t v, float acc) {
