@@ -356,7 +356,7 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
 #pragma unroll
     for (int hg = 0; hg < HG; ++hg) {
       float f = 1.f;
-      if (need[hg]) {
+      if (__builtin_expect(need[hg] != 0, 0)) {
         const float mt = wave_max_over_groups(mx[hg]);
         const float mn = mt > m_ref[hg] + kRefSlack ? mt + kRefHeadroom : m_ref[hg];
         f = __builtin_amdgcn_exp2f(m_ref[hg] - mn);  // 0 when nothing was summed yet
@@ -396,7 +396,7 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
       for (int i = 1; i < 8; ++i) mx[hg] = fmaxf(mx[hg], x[hg][i]);
       need[hg] = __builtin_amdgcn_ballot_w64(!first && mx[hg] > m_ref[hg] + kRefSlack);
     }
-    if (first) {
+    if (__builtin_expect(first, 0)) {
 #pragma unroll
       for (int hg = 0; hg < HG; ++hg) m_ref[hg] = wave_max_over_groups(mx[hg]) + kRefHeadroom;
     }
@@ -551,7 +551,7 @@ __global__ __launch_bounds__(kThreads, 1) void decode_stage1(DecodeArgs a) {
       for (int mb = 0; mb < 2; ++mb) S[mb][0] += S2[mb][0];
     }
     float x[HG][8];
-    if (base >= lo && base + kTile <= hi)  // an interior tile: every token is an INT2 one
+    if (__builtin_expect(base >= lo && base + kTile <= hi, 1))  // an interior tile: every token is an INT2 one
       masked(S, [](int) { return true; }, x);
     else
       masked(S, [&](int tok) { return base + tok >= lo && base + tok < hi; }, x);
