@@ -29,9 +29,10 @@
 //              query converted to fp16 once (exact products, FP32
 //              accumulate); rope on bf16 MFMA into the same accumulators;
 //   softmax    FP32 in the log2 domain against a per-wave reference per head
-//              (the first tile's maximum); a tile whose maximum passes it by
-//              more than 15 moves it there and scales O and the sum by the
-//              difference, so every probability is at most 2^15;
+//              (the first tile's maximum + 8); a tile whose maximum passes it
+//              by more than 15 moves it to that maximum + 8 and scales O and
+//              the sum by the difference, so every probability is at most
+//              2^15;
 //   output     O[head, f] += P V on fp16 MFMA (P rounded to fp16: relative
 //              error 2^-12 per probability) with V read transposed out of the
 //              wave's LDS copy of the expanded tile (ds_read_b64_tr_b16).
