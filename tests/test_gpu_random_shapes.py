@@ -16,7 +16,7 @@ from tests.test_gpu_extend import run_case
 pytestmark = pytest.mark.gpu
 
 ROPE = {512: 64, 256: 32}
-HEADS = [1, 5, 8, 16, 20, 24, 40]
+HEADS = [1, 5, 8, 16, 20, 24, 40, 48, 64, 128]
 PAGES = [1, 16, 32, 64]
 WINDOWS = [(4, 16), (4, 8), (0, 0)]
 EDGES = [1, 2, 3, 20, 31, 32, 33, 63, 64, 65, 127, 128, 129]
@@ -26,7 +26,7 @@ def _length(g, lo, hi):
     return int(g.choice(EDGES)) if g.random() < 0.4 else int(g.integers(lo, hi))
 
 
-@pytest.mark.parametrize("seed", range(10))
+@pytest.mark.parametrize("seed", range(48))
 def test_decode_random_shapes(seed):
     g = np.random.default_rng(1000 + seed)
     D = int(g.choice([512, 256]))
@@ -45,7 +45,7 @@ def test_decode_random_shapes(seed):
     check_against_oracle(pool, q, out, lse, slots, lengths, reqs, splits, P, W, sm_scale, D, max_splits=16)
 
 
-@pytest.mark.parametrize("seed", range(8))
+@pytest.mark.parametrize("seed", range(24))
 def test_extend_random_shapes(seed):
     g = np.random.default_rng(2000 + seed)
     D = int(g.choice([512, 256]))
