@@ -2,7 +2,12 @@
 north-star tolerance (rtol 2e-2, atol 2e-3): head counts, latent widths,
 batch sizes, lengths (tile and page boundaries drawn often), page sizes,
 split counts and the reference's window presets (mla_quant/common.py:16)
-come from fixed generators, so every run checks the same cases."""
+come from fixed generators, so every run checks the same cases. The fused
+writer on random chunked-prefill launches (several requests' chunks at random
+offsets in one launch, rows in shuffled slots, a request without ring rows)
+against the oracle's writer (mla_fused_writer.py:16-51,110-224): codes within
+the +-1 flip budget, params to FP32 rounding, rope and the ring maps exact,
+window rows within one bf16 rounding."""
 import math
 
 import numpy as np
@@ -12,6 +17,9 @@ import torch
 from tests.helpers import build_pool, make_queries, pool_to_gpu
 from tests.test_gpu_decode import ATOL, RTOL, check_against_oracle, run_decode
 from tests.test_gpu_extend import run_case
+from tests.test_gpu_writer import _compare_layer
+from oracle import codec, window
+from mla_kv_quant_amd import PackedMLAPool, synth, writer
 
 pytestmark = pytest.mark.gpu
 
@@ -59,3 +67,42 @@ def test_extend_random_shapes(seed):
     out, ref = run_case(D, R, H, prefixes, chunks, page, seed=90 + seed, P=P, W=W)
     assert torch.isfinite(out).all()
     torch.testing.assert_close(out.double(), ref, rtol=RTOL, atol=ATOL)
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_writer_random_chunks(seed):
+    g = np.random.default_rng(3000 + seed)
+    D = int(g.choice([512, 256]))
+    R = ROPE[D]
+    P, W = WINDOWS[int(g.integers(0, len(WINDOWS)))]
+    nreq = int(g.integers(1, 6))
+    max_reqs = nreq + 1
+    quant = None if g.random() < 0.5 else (float(g.uniform(0.6, 1.2)),)
+    if quant is not None:
+        quant = (quant[0], codec.signal_gain(quant[0]))
+    t, gain = quant if quant is not None else (writer.LM_THRESHOLD, writer.LM_GAIN)
+    size = 4096
+    rot = synth.make_rotation(D, 500 + seed)
+    pool = PackedMLAPool(size, 1, D, R, max_reqs, P, W, device="cuda", rotations=[rot], quantizers=[quant])
+    ref = window.new_pool(size + 1, D, R, max_reqs, P, W)
+    free = list(g.permutation(np.arange(1, size + 1)))
+    loc, pos, seq, req = [], [], [], []
+    for b in range(nreq):
+        start = 0 if g.random() < 0.4 else _length(g, 1, 600)
+        n = _length(g, 1, 300)
+        r = b + 1 if b + 1 < max_reqs else max_reqs  # the last request index has no ring rows
+        r = max_reqs if g.random() < 0.15 else r
+        loc += [int(free.pop()) for _ in range(n)]
+        pos += list(range(start, start + n))
+        seq += [start + n] * n
+        req += [r] * n
+    loc, pos, seq, req = (np.array(v, np.int64) for v in (loc, pos, seq, req))
+    n = len(loc)
+    print(f"writer seed {seed}: D={D} P={P} W={W} rows={n} quant={quant}", flush=True)
+    x = synth.make_latent(n, D, 5, seed=7000 + seed)
+    pe = synth.make_normal((n, R), 8000 + seed)
+    window.write_rows(ref, x, pe, loc, seq, req, rot, t, gain, P, W, max_reqs, positions=pos)
+    writer.write_prefill(pool, 0, torch.from_numpy(loc).cuda(), x.cuda(), pe.cuda(), torch.from_numpy(pos).cuda(),
+                         torch.from_numpy(seq).cuda(), torch.from_numpy(req).cuda())
+    torch.cuda.synchronize()
+    _compare_layer(pool, 0, ref, loc, 1e-4)
