@@ -244,6 +244,22 @@ def test_long_context(page, splits):
                          sm, D, max_splits=4)
 
 
+@pytest.mark.parametrize("D,R,H", [(512, 64, 16), (256, 32, 40)], ids=["dsv2", "minicpm3"])
+def test_128k_context(D, R, H):
+    """A 128K-token request beside a 70K one: one split (4097 units, 1025
+    tiles for the longest wave) and the reference's 129 requested splits
+    (capped by the fused call), against the fp64 oracle."""
+    P, W = 4, 16
+    lengths = [131072 + 5, 70000]
+    gp, slots, pages, reqs = gpu_written_pool(lengths, D, R, P, W, 64, seed=61)
+    sm = 1 / math.sqrt(192 if D == 512 else 96)
+    q = make_queries(len(lengths), H, D, R, sm, seed=63)
+    pool = gpu_pool_to_oracle(gp)
+    for splits in ([1, 1], [129, 129]):
+        out, logits, lse = run_decode(gp, q, slots, pages, lengths, reqs, 64, splits, 129, P, W, sm)
+        check_against_oracle(pool, q, out, lse, slots, lengths, reqs, splits, P, W, sm, D, max_splits=129)
+
+
 @pytest.mark.parametrize("factor", [100.0, 1000.0])
 def test_query_outlier_channels(factor):
     """One query channel per 128-group scaled by 100 or 1000: the products of
