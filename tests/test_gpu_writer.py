@@ -221,3 +221,37 @@ def test_writer_request_index_beyond_32_bits_has_no_ring_rows():
     assert (b["row"][1:] == -1).all()
     for k in ("codes", "params", "rope", "row"):
         assert torch.equal(a[k], b[k]), k
+
+
+@pytest.mark.parametrize("D,R", [(512, 64), (256, 32)])
+def test_row_local_batching_is_exact(D, R):
+    """The quantizer is row-local (mla_quant/cache.py:188-202,1142-1159): one
+    launch over 200K rows and launches over random slices of them (tile and
+    stripe boundaries anywhere) store the same bytes in every pool buffer."""
+    P, W = 4, 16
+    lengths = [1, 17, 1000, 64 * 1000 + 3, 2049, 130_000 - 70]
+    n = sum(lengths)
+    size = n + 8
+    max_reqs = len(lengths) + 1
+    rot = [synth.make_rotation(D, 401)]
+    quant = [(0.9, codec.signal_gain(0.9))]
+    pools = [PackedMLAPool(size, 1, D, R, max_reqs, P, W, device=DEV, rotations=rot, quantizers=quant)
+             for _ in range(2)]
+    rng = np.random.default_rng(403)
+    loc = torch.from_numpy(rng.permutation(np.arange(1, size + 1))[:n].astype(np.int64)).to(DEV)
+    pos = torch.cat([torch.arange(L, device=DEV) for L in lengths])
+    seq = torch.cat([torch.full((L,), L, device=DEV) for L in lengths])
+    req = torch.cat([torch.full((L,), i + 1, device=DEV) for i, L in enumerate(lengths)])
+    x = synth.make_latent(n, D, 5, seed=404, device=DEV)
+    pe = synth.make_normal((n, R), 405, device=DEV)
+    writer.write_prefill(pools[0], 0, loc, x, pe, pos, seq, req)
+    cuts = [0, *sorted(rng.choice(np.arange(1, n), size=9, replace=False).tolist()), n]
+    for a, b in zip(cuts[:-1], cuts[1:]):
+        writer.write_prefill(pools[1], 0, loc[a:b], x[a:b], pe[a:b], pos[a:b], seq[a:b], req[a:b])
+    torch.cuda.synchronize()
+    for name in ("c_codes", "c_params", "rope_buf", "hp_c"):
+        u, v = getattr(pools[0], name)[0], getattr(pools[1], name)[0]
+        assert torch.equal(u.view(torch.uint8), v.view(torch.uint8)), name
+    assert torch.equal(pools[0].hp_row_of_slot, pools[1].hp_row_of_slot)
+    assert torch.equal(pools[0].hp_owner_of_row, pools[1].hp_owner_of_row)
+    assert int((pools[0].hp_row_of_slot >= 0).sum()) == sum(min(L, P + W) for L in lengths)
