@@ -328,3 +328,40 @@ def test_rescale_when_scores_outgrow_the_reference(win):
     out, logits, lse = run_decode(gp, q, slots, pages, lengths, reqs, 64, [2, 3], 4, P, W, sm)
     assert torch.isfinite(out).all()
     check_against_oracle(pool, q, out, lse, slots, lengths, reqs, [2, 3], P, W, sm, D, max_splits=4)
+
+
+@pytest.mark.parametrize("D,R,H", [(512, 64, 16), (256, 32, 40)], ids=["dsv2", "minicpm3"])
+def test_output_independent_of_page_layout(D, R, H):
+    """The same tokens stored in other physical places -- another page size,
+    another page shuffle, other request (ring) indices -- are the same values
+    in the same order to the kernel, so outputs and LSEs agree bit for bit."""
+    P, W = 4, 16
+    lengths = [3000, 77, 1, 640]
+    n = sum(lengths)
+    x = synth.make_latent(n, D, max(1, D // 100), seed=71, device=DEV)
+    pe = synth.make_normal((n, R), 72, device=DEV)
+    rt = synth.make_rotation(D, 73).to(torch.bfloat16).t().contiguous().to(DEV)
+    sm = 1 / math.sqrt(192 if D == 512 else 96)
+    q = make_queries(len(lengths), H, D, R, sm, seed=74)
+    results = []
+    for page, seed, reqs in ((64, 5, [1, 2, 3, 4]), (16, 6, [4, 1, 3, 2]), (1, 7, [2, 4, 1, 3])):
+        slots, pages, num_slots = alloc_slots(lengths, page, seed)
+        max_reqs = len(lengths) + 1
+        hp_rows = 1 + max_reqs * (P + W)
+        gp = {"codes": torch.zeros(num_slots, D // 4, dtype=torch.uint8, device=DEV),
+              "params": torch.zeros(num_slots, D // 128, 2, dtype=torch.float32, device=DEV),
+              "rope": torch.zeros(num_slots, R, dtype=torch.bfloat16, device=DEV),
+              "hp": torch.zeros(hp_rows, D, dtype=torch.bfloat16, device=DEV),
+              "row_of_slot": torch.full((num_slots,), -1, dtype=torch.int32, device=DEV),
+              "owner_of_row": torch.zeros(hp_rows, dtype=torch.int32, device=DEV)}
+        loc = torch.from_numpy(np.concatenate(slots)).to(DEV)
+        pos = torch.from_numpy(np.concatenate([np.arange(L) for L in lengths])).to(DEV)
+        seq = torch.from_numpy(np.concatenate([np.full(L, L) for L in lengths])).to(DEV)
+        rq = torch.from_numpy(np.concatenate([np.full(L, r) for L, r in zip(lengths, reqs)])).to(DEV)
+        kernels.write_rows(x, pe, rt, loc, seq, pos, rq, gp["codes"], gp["params"], gp["rope"], gp["hp"],
+                           gp["row_of_slot"], gp["owner_of_row"], P, W, max_reqs, 0.9810652732849121, 1.16)
+        out, logits, lse = run_decode(gp, q, slots, pages, lengths, reqs, page, [5, 2, 1, 3], 8, P, W, sm)
+        results.append((out, lse))
+    for out, lse in results[1:]:
+        assert torch.equal(out, results[0][0])
+        assert torch.equal(lse.nan_to_num(0.0), results[0][1].nan_to_num(0.0))
