@@ -160,6 +160,30 @@ def test_extend_unrotated_outlier_keys_no_worse_than_the_reference():
     assert outside <= 1e-4
 
 
+def test_extend_rotated_keys_cancellation_tail():
+    """A case from a wider seeded sweep (128 heads, rotated keys, s4r8): one
+    output element of 6.3 M, of magnitude 0.007 where its keys' values cancel,
+    lands 2.6e-3 from float64 against a bar of 2.15e-3 -- the fp16
+    probabilities' 2^-12 relative rounding times |v|. The reference's BF16
+    eager attention misses the bar on about 12 % of this case's elements:
+    the kernel's largest and RMS errors stay at or below the reference's,
+    every element stays within twice the bar, and at most 1e-6 of the
+    elements pass the bar itself."""
+    D, R, H, page = 256, 32, 128, 32
+    prefixes, chunks = [1020, 31, 300], [47, 71, 74]
+    out, ref = run_case(D, R, H, prefixes, chunks, page, seed=217, P=4, W=8)
+    _, eager = run_case(D, R, H, prefixes, chunks, page, seed=217, P=4, W=8, flavour="bf16_eager")
+    assert torch.isfinite(out).all()
+    err, err_ref = (out.double() - ref).abs(), (eager.double() - ref).abs()
+    bar = ATOL + RTOL * ref.abs()
+    assert err.max() <= err_ref.max()
+    assert err.pow(2).mean().sqrt() <= err_ref.pow(2).mean().sqrt()
+    assert (err <= 2 * bar).all()
+    outside = (err > bar).double().mean().item()
+    print(f"max|err| {err.max():.2e} (reference bf16: {err_ref.max():.2e}), beyond the bar: {outside:.2e}")
+    assert outside <= 1e-6
+
+
 def test_extend_short_workspace():
     """A workspace shorter than the key rows the caller states is rejected
     before any launch (ValueError, output untouched); a caller that states too
