@@ -269,3 +269,51 @@ def test_extend_hf_chunk_semantics():
         ref, _ = attention.extend(pool, q[s:e, :, :D], q[s:e, :, D:], lat32, pe[pf:L], slots[b][:pf], pf,
                                   int(reqs[b]), P, W, sm, D, chunk_mode="qdq", dtype=torch.float64)
         torch.testing.assert_close(out[s:e].double(), ref, rtol=RTOL, atol=ATOL)
+
+
+@pytest.mark.parametrize("D,R,H", [(512, 64, 16), (256, 32, 40)], ids=["dsv2", "minicpm3"])
+def test_extend_output_independent_of_page_layout(D, R, H):
+    """The same prefix tokens stored in other physical places (page sizes 64,
+    16 and 1, other shuffles, other request indices) give the same extend
+    output bits: the gather hands the attention the same rows in the same
+    order."""
+    from tests.helpers import alloc_slots
+    P, W = 4, 16
+    prefixes, chunks = [700, 0, 65], [40, 9, 70]
+    n = sum(prefixes)
+    sm = 1.0 / math.sqrt(96 if D == 256 else 192)
+    x = synth.make_latent(n, D, 3, seed=81, device=DEV)
+    pe = synth.make_normal((n, R), 82, device=DEV)
+    rt = synth.make_rotation(D, 83).to(torch.bfloat16).t().contiguous().to(DEV)
+    T = sum(chunks)
+    q = synth.make_normal((T, H, D + R), 84, std=2.0 / (sm * math.sqrt(D + R))).to(DEV)
+    kc = synth.make_normal((T, D + R), 85).to(DEV)
+    qo = torch.tensor(np.concatenate([[0], np.cumsum(chunks)]), dtype=torch.int32, device=DEV)
+    outs = []
+    for page, seed, reqs in ((64, 5, [1, 2, 3]), (16, 6, [3, 1, 2]), (1, 7, [2, 3, 1])):
+        slots, pages, num_slots = alloc_slots(prefixes, page, seed)
+        max_reqs = len(prefixes) + 1
+        hp_rows = 1 + max_reqs * (P + W)
+        codes = torch.zeros(num_slots, D // 4, dtype=torch.uint8, device=DEV)
+        params = torch.zeros(num_slots, D // 128, 2, dtype=torch.float32, device=DEV)
+        rope = torch.zeros(num_slots, R, dtype=torch.bfloat16, device=DEV)
+        hp = torch.zeros(hp_rows, D, dtype=torch.bfloat16, device=DEV)
+        row = torch.full((num_slots,), -1, dtype=torch.int32, device=DEV)
+        owner = torch.zeros(hp_rows, dtype=torch.int32, device=DEV)
+        live = [b for b in range(len(prefixes)) if prefixes[b] > 0]
+        loc = torch.from_numpy(np.concatenate([slots[b] for b in live])).to(DEV)
+        pos = torch.from_numpy(np.concatenate([np.arange(prefixes[b]) for b in live])).to(DEV)
+        seq = torch.from_numpy(np.concatenate([np.full(prefixes[b], prefixes[b]) for b in live])).to(DEV)
+        rq = torch.from_numpy(np.concatenate([np.full(prefixes[b], reqs[b]) for b in live])).to(DEV)
+        kernels.write_rows(x, pe, rt, loc, seq, pos, rq, codes, params, rope, hp, row, owner, P, W, max_reqs,
+                           0.9810652732849121, 1.16)
+        indptr, indices = index_lists(slots, pages, page)
+        out = torch.full((T, H, D), float("nan"), dtype=torch.bfloat16, device=DEV)
+        kernels.extend_fwd(q, kc, qo, indptr, indices, torch.tensor(prefixes, dtype=torch.int64, device=DEV),
+                           torch.tensor(reqs, dtype=torch.int64, device=DEV), codes, params, rope, hp, max(chunks),
+                           out, sm, P, W, page, max_reqs=max_reqs)
+        torch.cuda.synchronize()
+        outs.append(out.cpu())
+    assert torch.isfinite(outs[0].float()).all()
+    for o in outs[1:]:
+        assert torch.equal(o.view(torch.int16), outs[0].view(torch.int16))
